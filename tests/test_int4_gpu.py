@@ -1,0 +1,137 @@
+"""GPU parity of the int4 W4A16 path against the CPU oracle (oracle/int4.py).
+
+Bar: dequantized weights bit-exact; GEMM max|y - ref| <= 1e-2 * max|ref|
+(fp32-accumulated reference, fp16/bf16 output), the north-star tolerance.
+Shapes: BASELINE config 0 (fp16, M=16, K=N=4096, seed 0), config 1 (bf16,
+gate_up K=4096 N=28672 and down K=14336 N=4096, M in {1, 8, 32, 128}), ragged
+M, the reference test's shapes (tests/test_marlin_int4.py:52-70).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import int4 as oint4
+from oracle.numerics import round_to
+from tests._problems import int4_problem, to_np32
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _setup(m, k, n, dtype, seed, dev):
+    from torchinferno_amd.kernels import int4 as ti4
+    a, codes, scales = int4_problem(m, k, n, dtype, seed)
+    qweight = ti4.pack_int4(codes)
+    pw, ps = ti4.repack_int4(qweight.to(dev), scales.to(dev))
+    ws = ti4.make_workspace(n, dev, size_k=k, max_m=max(m, 1))
+    return a, qweight, scales, pw, ps, ws
+
+
+def _rel_err(y, ref):
+    return float(np.abs(y - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_dequant_bit_exact(dev, dtype):
+    from torchinferno_amd.kernels import int4 as ti4
+    k, n = 512, 192
+    _, qweight, scales, pw, ps, _ = _setup(1, k, n, dtype, 7, dev)
+    got = ti4.dequantize_int4(pw, ps, k, n).cpu().numpy()
+    ref = oint4.dequant_int4(qweight.numpy(), to_np32(scales))
+    assert got.dtype == np.float32
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def _run_gemm(dev, m, k, n, dtype, seed):
+    from torchinferno_amd.kernels import int4 as ti4
+    a, qweight, scales, pw, ps, ws = _setup(m, k, n, dtype, seed, dev)
+    out = ti4.int4_mm(a.to(dev), pw, ps, ws, n, k)
+    torch.cuda.synchronize()
+    ref = oint4.w4a16_reference(to_np32(a), qweight.numpy(), to_np32(scales))
+    return out, ref
+
+
+@pytest.mark.parametrize("m", [16])
+def test_config0_fp16(dev, m):
+    print(f"[int4] config0 M={m}", flush=True)
+    out, ref = _run_gemm(dev, m, 4096, 4096, torch.float16, 0)
+    assert out.dtype == torch.float16 and out.shape == (m, 4096)
+    err = _rel_err(out.float().cpu().numpy(), ref)
+    assert err <= TOL, err
+    # Output rounding bound: a correct kernel is within a few fp16 ulps of the
+    # rounded fp32 reference.
+    assert err <= 2e-3, err
+
+
+@pytest.mark.parametrize("k,n", [(4096, 28672), (14336, 4096)])
+@pytest.mark.parametrize("m", [1, 8, 32, 128])
+def test_config1_bf16(dev, m, k, n):
+    print(f"[int4] config1 M={m} K={k} N={n}", flush=True)
+    out, ref = _run_gemm(dev, m, k, n, torch.bfloat16, 1)
+    err = _rel_err(out.float().cpu().numpy(), ref)
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("m", [1, 2, 15, 17, 33, 63, 65, 100, 129, 200])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_ragged_m(dev, m, dtype):
+    print(f"[int4] ragged M={m} {dtype}", flush=True)
+    out, ref = _run_gemm(dev, m, 1024, 320, dtype, 100 + m)
+    err = _rel_err(out.float().cpu().numpy(), ref)
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("n,k", [(7168, 8192), (8192, 3584)])
+def test_reference_marlin_shapes_rtn(dev, n, k):
+    """tests/test_marlin_int4.py:52-70: RTN-quantized w = randn*0.02, a = randn(48, K),
+    seed 0, mean-abs relative error < 0.03 vs the dequant reference of the *original*
+    weights' quantization."""
+    from torchinferno_amd.kernels import int4 as ti4
+    print(f"[int4] reference shape N={n} K={k}", flush=True)
+    g = torch.Generator().manual_seed(0)
+    w = (torch.randn(k, n, generator=g) * 0.02).to(torch.bfloat16)
+    a = torch.randn(48, k, generator=g).to(torch.bfloat16)
+    q, s = ti4.quantize_int4_rtn(w, 128, torch.bfloat16)
+    oq, os_ = oint4.quantize_int4_rtn(round_to(w.float().numpy(), "fp16"), 128, "bf16")
+    assert np.array_equal(q.numpy(), oq)
+    assert np.array_equal(s.float().numpy(), os_)
+    pw, ps = ti4.repack_int4(q.to(dev), s.to(dev))
+    ws = ti4.make_workspace(n, dev, size_k=k, max_m=48)
+    out = ti4.marlin_int4_mm(a.to(dev), pw, ps, ws, n, k).float().cpu().numpy()
+    ref = oint4.w4a16_reference(to_np32(a), oq, os_)
+    rel = np.abs(out - ref).mean() / np.abs(ref).mean()
+    assert rel < 0.03
+    assert _rel_err(out, ref) <= TOL
+
+
+def test_out_buffer_contract_and_workspace_reuse(dev):
+    """Caller-owned out is written in place (tests/test_marlin_int4.py:15-37); a
+    shared workspace stays valid across calls of different M (ticket reset)."""
+    from torchinferno_amd.kernels import int4 as ti4
+    k, n = 14336, 4096
+    a, qweight, scales, pw, ps, ws = _setup(32, k, n, torch.bfloat16, 3, dev)
+    ad = a.to(dev)
+    out = torch.empty((32, n), dtype=torch.bfloat16, device=dev)
+    ptr = out.data_ptr()
+    r1 = ti4.int4_mm(ad, pw, ps, ws, n, k, out=out)
+    assert r1 is out and out.data_ptr() == ptr
+    first = out.clone()
+    r2 = ti4.int4_mm(ad[:5].contiguous(), pw, ps, ws, n, k)
+    r3 = ti4.int4_mm(ad, pw, ps, ws, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(first, r3), "nondeterministic or workspace not reset"
+    assert torch.equal(r2, first[:5])
+    with pytest.raises(ValueError):
+        ti4.int4_mm(ad, pw, ps, ws, n, k, out=torch.empty((32, n), dtype=torch.float16, device=dev))
+
+
+def test_unsupported_shape_raises(dev):
+    from torchinferno_amd import _lib
+    from torchinferno_amd.kernels import int4 as ti4
+    assert not ti4.int4_supports_shape(16032, 8192)
+    a = torch.zeros((4, 256), dtype=torch.bfloat16, device=dev)
+    pw = torch.zeros((100 * 256 // 8,), dtype=torch.int32, device=dev)
+    ps = torch.zeros((2, 100), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(_lib.TiUnsupported):
+        ti4.int4_mm(a, pw, ps, None, 100, 256)
