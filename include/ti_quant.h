@@ -70,10 +70,12 @@ int ti_int4_repack(const int32_t* qweight, const void* scales, int scale_dtype,
 int ti_int4_dequant(const int32_t* packed_weight, const void* packed_scales, int scale_dtype,
                     int K, int N, int group_size, float* out, hipStream_t stream);
 
-/* Workspace bytes ti_w4a16_gemm needs for this problem (0 if none).  The
- * workspace must be zero-filled once when allocated; every call leaves it
- * zeroed again.  Calls sharing one workspace must be stream-ordered. */
+/* Workspace bytes ti_w4a16_gemm needs for this problem (0 if none), and for
+ * every M in [1, max_m] with one shared buffer.  The workspace must be
+ * zero-filled once when allocated; every call leaves its ticket words zero
+ * again.  Calls sharing one workspace must be stream-ordered. */
 size_t ti_w4a16_workspace_bytes(int M, int N, int K, int group_size);
+size_t ti_w4a16_workspace_bytes_max(int max_m, int N, int K, int group_size);
 
 /* out[M, N] = a[M, K] @ dequant(W), fp32 accumulation, out in a's dtype.
  * Replaces torch.ops._C.marlin_gemm as called by marlin_int4_mm

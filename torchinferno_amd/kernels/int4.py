@@ -115,8 +115,8 @@ def make_workspace(size_n: int, device, *, size_k: int, max_m: int = 128,
                    group_size: int = GROUP_SIZE) -> Tensor:
     """Zero-filled workspace serving every M in [1, max_m] for an [K, N] weight.
     Kernels leave it zeroed; calls sharing it must be ordered on one stream."""
-    need = max(workspace_bytes(m, size_n, size_k, group_size) for m in range(1, max_m + 1))
-    return torch.zeros(max(1, (need + 3) // 4), dtype=torch.int32, device=device)
+    need = int(_lib.lib().ti_w4a16_workspace_bytes_max(max_m, size_n, size_k, group_size))
+    return torch.zeros(max(4, (need + 3) // 4), dtype=torch.int32, device=device)
 
 
 def int4_mm(a: Tensor, q_weight: Tensor, scales: Tensor, workspace: Tensor, size_n: int,
