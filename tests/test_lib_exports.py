@@ -35,7 +35,7 @@ def test_host_side_queries():
     assert lib.ti_int4_packed_weight_bytes(4096, 4096) == 4096 * 4096 // 2
     # Unsupported shapes report zero workspace and no crash.
     assert lib.ti_w4a16_workspace_bytes(1, 100, 256, 128) == 0
-    assert lib.ti_w4a16_workspace_bytes(1, 4096, 14336, 128) > 0
+    assert lib.ti_w4a16_workspace_bytes(16, 4096, 14336, 128) > 0  # split-K plan
 
 
 def test_gemm_rejects_bad_arguments_without_gpu():
