@@ -117,11 +117,18 @@ def test_out_buffer_contract_and_workspace_reuse(dev):
     r1 = ti4.int4_mm(ad, pw, ps, ws, n, k, out=out)
     assert r1 is out and out.data_ptr() == ptr
     first = out.clone()
-    r2 = ti4.int4_mm(ad[:5].contiguous(), pw, ps, ws, n, k)
+    a5 = ad[:5].contiguous()
+    r2 = ti4.int4_mm(a5, pw, ps, ws, n, k)
     r3 = ti4.int4_mm(ad, pw, ps, ws, n, k)
+    r4 = ti4.int4_mm(a5, pw, ps, ti4.make_workspace(n, dev, size_k=k, max_m=5), n, k)
     torch.cuda.synchronize()
     assert torch.equal(first, r3), "nondeterministic or workspace not reset"
-    assert torch.equal(r2, first[:5])
+    # Same M, shared vs fresh workspace: identical bits (fixed split order).
+    assert torch.equal(r2, r4)
+    # Different M may take a different split plan (another fp32 summation
+    # order), so rows agree to the output tolerance, not bit for bit.
+    ref = first[:5].float()
+    assert float((r2.float() - ref).abs().max() / ref.abs().max()) <= TOL
     with pytest.raises(ValueError):
         ti4.int4_mm(ad, pw, ps, ws, n, k, out=torch.empty((32, n), dtype=torch.float16, device=dev))
 
