@@ -223,7 +223,7 @@ def main():
     roofline = {
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-        "kernel": "ti::int4::w4a16_gemm_kernel<bf16, MT=2>",
+        "kernel": "ti::int4::w4a16_decode_kernel<bf16, MR=32, NT=4, WK=2, R=3, SPLIT=0>",
         "launch": "gate_up K=4096 N=28672 M=32",
         "avg_launch_us": round(t_head * 1e6, 2),
         "algo_bytes_per_launch": head.algo_bytes,

@@ -142,3 +142,28 @@ def test_unsupported_shape_raises(dev):
     ps = torch.zeros((2, 100), dtype=torch.bfloat16, device=dev)
     with pytest.raises(_lib.TiUnsupported):
         ti4.int4_mm(a, pw, ps, None, 100, 256)
+
+
+@pytest.mark.parametrize("k,n", [(4096, 28672), (14336, 4096)])
+@pytest.mark.parametrize("m", [24, 48, 64])
+def test_decode_kernel_rows(dev, m, k, n):
+    """Rows 17..64 run the LDS-DMA decode kernel (int4_decode.hip)."""
+    print(f"[int4] decode M={m} K={k} N={n}", flush=True)
+    out, ref = _run_gemm(dev, m, k, n, torch.bfloat16, 11)
+    assert _rel_err(out.float().cpu().numpy(), ref) <= TOL
+
+
+# Every template variant of the decode kernel, forced through the plan override
+# ("nt:wk:ring:splits"), on a ragged problem; rows 3 / 13 / 29 stage 4 / 16 / 32 rows.
+_DECODE_PLANS = ["1:1:3:1", "2:1:4:3", "4:1:6:1", "1:2:3:2", "2:2:6:1", "4:2:4:2",
+                 "1:4:4:1", "2:4:3:4", "4:4:3:1"]
+
+
+@pytest.mark.parametrize("plan", _DECODE_PLANS)
+@pytest.mark.parametrize("m", [3, 13, 29, 45])
+def test_decode_kernel_plans(dev, monkeypatch, plan, m):
+    print(f"[int4] decode plan {plan} M={m}", flush=True)
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MIN_M", "1")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_PLAN", plan)
+    out, ref = _run_gemm(dev, m, 2048, 512, torch.float16 if m % 2 else torch.bfloat16, 20 + m)
+    assert _rel_err(out.float().cpu().numpy(), ref) <= TOL

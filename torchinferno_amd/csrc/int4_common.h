@@ -1,0 +1,91 @@
+// Device helpers shared by the int4 W4A16 kernels (int4_gemm.hip, int4_decode.hip):
+// the in-register nibble unpack, the bf16/fp16 MFMA step, and the per-group
+// compute of one wave (bias-corrected MFMA sums scaled into fp32 accumulators).
+#pragma once
+
+#include "ti_common.h"
+
+namespace ti {
+namespace int4 {
+
+constexpr int kGroup = 128;
+
+template <int DT>
+struct Magic;
+template <>
+struct Magic<TI_DTYPE_F16> {
+  static constexpr uint32_t kOr = 0x64006400u;            // 1024 + q
+  static constexpr float kBias = 1032.0f;                 // 1024 + zero point 8
+  static constexpr uint32_t kNegBiasPair = 0xE408E408u;   // fp16 -1032 x2
+};
+template <>
+struct Magic<TI_DTYPE_BF16> {
+  static constexpr uint32_t kOr = 0x43004300u;            // 128 + q
+  static constexpr float kBias = 136.0f;                  // 128 + zero point 8
+  static constexpr uint32_t kNegBiasPair = 0xC308C308u;   // bf16 -136 x2
+};
+
+// (x & mask) | magic in one v_and_or_b32 (the compiler otherwise splits it).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm volatile("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(mask), "v"(magic));
+  return r;
+}
+
+template <int DT>
+__device__ __forceinline__ i32x4 unpack8(uint32_t w, uint32_t mask, uint32_t magic) {
+  i32x4 r;
+  r[0] = (int)and_or(w, mask, magic);
+  r[1] = (int)and_or(w >> 4, mask, magic);
+  r[2] = (int)and_or(w >> 8, mask, magic);
+  r[3] = (int)and_or(w >> 12, mask, magic);
+  return r;
+}
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16x16x32(i32x4 a, i32x4 b, f32x4 c) {
+  if constexpr (DT == TI_DTYPE_F16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float scale_to_f32(uint32_t bits) {
+  return DT == TI_DTYPE_F16 ? f16_bits_to_f32((uint16_t)bits) : bf16_bits_to_f32((uint16_t)bits);
+}
+
+template <int DT, int MT, int NT>
+__device__ __forceinline__ void compute_group(const i32x4 (&w)[NT], const i32x4 (&a)[MT][4],
+                                              const float (&sc)[NT], f32x4 (&acc)[NT][MT]) {
+  const uint32_t mask = 0x000F000Fu, magic = Magic<DT>::kOr;
+  const i32x4 negbias = {(int)Magic<DT>::kNegBiasPair, (int)Magic<DT>::kNegBiasPair,
+                         (int)Magic<DT>::kNegBiasPair, (int)Magic<DT>::kNegBiasPair};
+  f32x4 nbias[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    nbias[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) nbias[mt] = mfma16x16x32<DT>(a[mt][j], negbias, nbias[mt]);
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    i32x4 b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = unpack8<DT>((uint32_t)w[t][j], mask, magic);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      f32x4 cc = nbias[mt];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cc = mfma16x16x32<DT>(a[mt][j], b[j], cc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[t][mt][i] = __builtin_fmaf(sc[t], cc[i], acc[t][mt][i]);
+    }
+  }
+}
+
+}  // namespace int4
+}  // namespace ti

@@ -1,0 +1,363 @@
+// int4 W4A16 decode kernel for gfx950: the skinny-M (M <= 32 per row chunk)
+// path of ti_w4a16_gemm.  Same arithmetic and weight layout as int4_gemm.hip
+// (blocks of 16 columns x 128 rows, one 1 KiB block per wave-load, in-register
+// magic-number unpack, bias-corrected MFMA sums scaled in fp32); what differs
+// is how operands reach the waves.
+//
+// Every operand travels HBM/L2 -> LDS by direct LDS DMA
+// (global_load_lds_dwordx4 / _dword), issued from inline asm so that this
+// kernel, not the compiler, accounts the in-order vmcnt counter:
+//   * weights: a wave's NT blocks of the next group, each a fully coalesced
+//     1 KiB read that lands lane-linear in LDS (read back lane-linear);
+//   * activations: the MP (16 or 32) rows x 128 K of the group, read with
+//     coalesced 256 B row segments and stored XOR-swizzled (16-byte chunk q of
+//     row r at slot r*16 + (q ^ (r & 15))), so the MFMA operand read -- lane
+//     l takes row l%16, chunk l/16 + 4j -- is bank-conflict free;
+//   * scales: the workgroup's [groups x columns] slab once, in the prologue.
+// A ring of R LDS stages keeps R-1 groups in flight per wave without holding
+// them in VGPRs.  One step: wait for the own DMAs of the current stage
+// (s_waitcnt vmcnt(#later stages * per-stage count)), s_barrier (all waves'
+// DMAs landed, and everyone finished the previous stage, whose buffer is the
+// one refilled next), issue the DMAs of step i+R-1, compute step i.
+//
+// Workgroup = 4 waves = WK (K ranges) x WN (column sets).  Waves that share a
+// K range share its activation stage; the WK partial sums are added through
+// LDS in wk order at the end.  Across workgroups, `splits` K ranges are summed
+// by the last-arriving workgroup of a column block in split order (agent-scope
+// stores and loads of fp32 partials + a ticket), so results are deterministic.
+#include "int4_decode.h"
+
+namespace ti {
+namespace int4 {
+
+namespace {
+
+constexpr int kWaves = 4;
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// 16 bytes per lane, global -> LDS at lds_base + 16 * lane.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base))
+               : "memory");
+}
+
+// 4 bytes per lane, global -> LDS at lds_base + 4 * lane.
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :
+               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base))
+               : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+template <int DT, int MR, int NT, int WK, int R, int SPLIT>
+__global__ __launch_bounds__(64 * kWaves) void w4a16_decode_kernel(
+    const uint16_t* __restrict__ A, const i32x4* __restrict__ Wp, const uint16_t* __restrict__ Sg,
+    uint16_t* __restrict__ out, float* __restrict__ partial, int* __restrict__ tickets, int M, int N,
+    int K, int splits) {
+  constexpr int WN = kWaves / WK;
+  constexpr int MT = MR > 16 ? 2 : 1;            // 16-row MFMA tiles
+  constexpr int MP = MT * 16;                    // rows of one row chunk
+  constexpr int AI = WK * MR / 4;                // 1 KiB activation DMAs per stage (all waves)
+  constexpr int AI_LO = AI / kWaves;             // ... per wave: AI_LO or AI_HI
+  constexpr int AI_HI = (AI + kWaves - 1) / kWaves;
+  constexpr int P = R - 1;                       // stages in flight ahead of compute
+  constexpr int W_BYTES = kWaves * NT * 1024;    // weight blocks of one stage
+  constexpr int A_BYTES = MR * 256;              // one K range's activations of one stage
+  constexpr int STAGE = W_BYTES + WK * A_BYTES;
+  constexpr int WC = WN * NT * 16;               // columns of the workgroup
+  static_assert((NT + AI_HI) * P <= 63, "vmcnt holds at most 63 outstanding loads");
+
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int last_flag;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wk = wave / WN, wn = wave % WN;
+  const int nb = blockIdx.x, split = blockIdx.y, mchunk = blockIdx.z;
+  const int NG = K / kGroup;
+  const long T = N / 16;
+  const int m0 = mchunk * MP;
+  // Activation DMAs of this wave: ids wave, wave + 4, ... below AI.
+  const int a_cnt = (AI - wave + kWaves - 1) / kWaves;
+  const int col_base = nb * WC;
+  const long tile0 = (long)nb * (WN * NT) + wn * NT;
+
+  // K range of the workgroup: groups [g0, g1); wave range wk: g0 + wk*nper + i.
+  const int per_split = cdiv(NG, splits);
+  const int g0 = split * per_split;
+  const int g1 = min(NG, g0 + per_split);
+  const int ngr = max(g1 - g0, 0);
+  const int nper = cdiv(ngr, WK);
+  const int gmax = max(g1 - 1, 0);  // clamp target: any valid group
+
+  const uint32_t lds0 = lds_offset(smem);
+  const uint32_t ring0 = lds0;
+  const uint32_t sc0 = lds0 + R * STAGE;
+  const uint16_t* sS = (const uint16_t*)(smem + R * STAGE);
+
+  // ---- prologue: scales [ngr x WC] halves, dword DMA, 256 B per instruction ----
+  {
+    const int sbytes = ngr * WC * 2;
+    const int nch = cdiv(sbytes, 256);
+    for (int ch = wave; ch < nch; ch += kWaves) {
+      const int o = ch * 256 + lane * 4;
+      const uint16_t* src = Sg;
+      if (o < sbytes) {
+        const int gi = o / (WC * 2);
+        const int cb = (o % (WC * 2)) / 2;
+        src = Sg + (long)(g0 + gi) * N + col_base + cb;
+      }
+      dma4(src, sc0 + ch * 256);
+    }
+  }
+
+  // Issue the DMAs of step `i` into ring buffer i % R.
+  auto issue = [&](int i) {
+    const uint32_t base = ring0 + (uint32_t)((i % R) * STAGE);
+    const int g = min(g0 + wk * nper + i, gmax);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      dma16(&Wp[((long)g * T + tile0 + t) * 64 + lane], base + (uint32_t)((wave * NT + t) * 1024));
+#pragma unroll
+    for (int u = 0; u < AI_HI; ++u) {
+      const int id = wave + u * kWaves;        // 0 .. AI - 1
+      if (id >= AI) break;
+      const int awk = id / (MR / 4), k4 = id % (MR / 4);
+      const int r = 4 * k4 + (lane >> 4);
+      const int q = (lane & 15) ^ (r & 15);
+      const int ga = min(g0 + awk * nper + i, gmax);
+      const int row = min(m0 + r, M - 1);
+      dma16(A + (long)row * K + (long)ga * kGroup + q * 8,
+            base + (uint32_t)(W_BYTES + awk * A_BYTES + k4 * 1024));
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < P; ++s)
+    if (s < nper) issue(s);
+
+  f32x4 acc[NT][MT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int c = lane & 15, kq = lane >> 4;
+  for (int i = 0; i < nper; ++i) {
+    // Stages issued after stage i: min(P-1, nper-1-i).  Full-depth steps wait
+    // for exactly one stage; the last P-1 steps drain.
+    if (i + P - 1 < nper) {
+      if (a_cnt > AI_LO) wait_vm_barrier<(P - 1) * (NT + AI_HI)>();
+      else wait_vm_barrier<(P - 1) * (NT + AI_LO)>();
+    } else {
+      wait_vm_barrier<0>();
+    }
+    if (i + P < nper) issue(i + P);
+
+    const uint8_t* st = smem + (i % R) * STAGE;
+    const int g = g0 + wk * nper + i;
+    const bool valid = g < g1;
+    const int gl = valid ? g - g0 : 0;
+    i32x4 w[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) w[t] = *(const i32x4*)(st + (wave * NT + t) * 1024 + lane * 16);
+    i32x4 a[MT][4];
+    const uint8_t* ab = st + W_BYTES + wk * A_BYTES;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      // Rows past the staged MR repeat staged ones; their outputs are not stored.
+      const int r = (mt * 16 + c) % MR;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int q = 4 * j + kq;
+        a[mt][j] = *(const i32x4*)(ab + (r * 16 + (q ^ (r & 15))) * 16);
+      }
+    }
+    float sc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const float v = scale_to_f32<DT>(sS[gl * WC + (wn * NT + t) * 16 + c]);
+      sc[t] = valid ? v : 0.f;
+    }
+    compute_group<DT, MT, NT>(w, a, sc, acc);
+  }
+  // No DMA may still be writing LDS when it is reused or the workgroup ends.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- add the WK partial sums through LDS (fixed wk order) ----
+  float* red = (float*)smem;
+  if constexpr (WK > 1) {
+    __syncthreads();
+    if (wk > 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            red[((((wk - 1) * WN + wn) * NT + t) * MT + mt) * 256 + e * 64 + lane] = acc[t][mt][e];
+    }
+    __syncthreads();
+  }
+
+  const int rows = min(MP, M - m0);
+  if (wk == 0) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = acc[t][mt][e];
+#pragma unroll
+          for (int w2 = 1; w2 < WK; ++w2) v += red[((((w2 - 1) * WN + wn) * NT + t) * MT + mt) * 256 + e * 64 + lane];
+          const int row = mt * 16 + kq * 4 + e;
+          const int col = col_base + (wn * NT + t) * 16 + c;
+          if (row < rows) {
+            const long off = (long)(m0 + row) * N + col;
+            if constexpr (SPLIT == 0) out[off] = to_bits<DT>(v);
+            else __hip_atomic_store(&partial[(long)split * M * N + off], v, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+  }
+  if constexpr (SPLIT == 0) return;
+
+  // Partials are written through to memory once vmcnt drains; then the ticket.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  int* ticket = tickets + mchunk * gridDim.x + nb;
+  if (threadIdx.x == 0)
+    last_flag = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+  __syncthreads();
+  if (!last_flag) return;
+  for (int e = threadIdx.x; e < rows * WC; e += 64 * kWaves) {
+    const int r = e / WC;
+    const long off = (long)(m0 + r) * N + col_base + e % WC;
+    float v = 0.f;
+    for (int sp = 0; sp < splits; ++sp)
+      v += __hip_atomic_load(&partial[(long)sp * M * N + off], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    out[off] = to_bits<DT>(v);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int DT, int MR, int NT, int WK, int R>
+void launch_split(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
+  dim3 grid(p.nblocks, p.splits, p.mchunks);
+  if (p.splits == 1)
+    hipLaunchKernelGGL((w4a16_decode_kernel<DT, MR, NT, WK, R, 0>), grid, dim3(64 * kWaves), p.lds,
+                       stream, x.a, x.w, x.s, x.out, x.partial, x.tickets, x.M, x.N, x.K, 1);
+  else
+    hipLaunchKernelGGL((w4a16_decode_kernel<DT, MR, NT, WK, R, 2>), grid, dim3(64 * kWaves), p.lds,
+                       stream, x.a, x.w, x.s, x.out, x.partial, x.tickets, x.M, x.N, x.K, p.splits);
+}
+
+template <int DT, int MR, int NT, int WK>
+void launch_r(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
+  if (p.ring == 3) launch_split<DT, MR, NT, WK, 3>(p, x, stream);
+  else if (p.ring == 4) launch_split<DT, MR, NT, WK, 4>(p, x, stream);
+  else launch_split<DT, MR, NT, WK, 6>(p, x, stream);
+}
+
+template <int DT, int MR, int NT>
+void launch_wk(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
+  if (p.wk == 1) launch_r<DT, MR, NT, 1>(p, x, stream);
+  else if (p.wk == 2) launch_r<DT, MR, NT, 2>(p, x, stream);
+  else launch_r<DT, MR, NT, 4>(p, x, stream);
+}
+
+template <int DT, int MR>
+void launch_nt(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
+  if (p.nt == 1) launch_wk<DT, MR, 1>(p, x, stream);
+  else if (p.nt == 2) launch_wk<DT, MR, 2>(p, x, stream);
+  else launch_wk<DT, MR, 4>(p, x, stream);
+}
+
+template <int DT>
+void launch_mr(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
+  if (p.mr == 4) launch_nt<DT, 4>(p, x, stream);
+  else if (p.mr == 16) launch_nt<DT, 16>(p, x, stream);
+  else launch_nt<DT, 32>(p, x, stream);
+}
+
+int stage_bytes(int mr, int nt, int wk) { return kWaves * nt * 1024 + wk * mr * 256; }
+
+// TI_ROCM_W4A16_DECODE_PLAN="nt:wk:ring:splits" overrides the heuristic (tuning).
+bool env_plan(DecodePlan& p) {
+  const char* e = getenv("TI_ROCM_W4A16_DECODE_PLAN");
+  if (!e || !*e) return false;
+  int nt, wk, r, s;
+  if (sscanf(e, "%d:%d:%d:%d", &nt, &wk, &r, &s) != 4) return false;
+  p.nt = nt; p.wk = wk; p.ring = r; p.splits = s;
+  return true;
+}
+
+}  // namespace
+
+DecodePlan make_decode_plan(int M, int N, int K) {
+  DecodePlan p;
+  p.mr = M <= 4 ? 4 : (M <= 16 ? 16 : 32);
+  p.mchunks = cdiv(M, p.mr > 16 ? 32 : 16);
+  const int NG = K / kGroup;
+  const int T = N / 16;
+  if (!env_plan(p)) {
+    // Measured on MI355X at the Llama-3-8B MLP shapes (decode rows 17..64):
+    // wide N (gate_up, N=28672) streams best with no split; narrow N (down,
+    // N=4096) needs all four waves on K and a 2-way split at M <= 32.
+    const bool wide = T >= 1024;
+    p.ring = wide && M > 32 ? 4 : 3;
+    if (wide) {
+      p.nt = M <= 32 ? 4 : 2;
+      p.wk = M <= 32 ? 2 : 1;
+      p.splits = 1;
+    } else {
+      p.nt = 2;
+      p.wk = 4;
+      const int blocks = T / (p.nt * (kWaves / p.wk));
+      p.splits = (M <= 32 && blocks * p.mchunks < 256) ? 2 : 1;
+    }
+  }
+  if (p.nt != 1 && p.nt != 2 && p.nt != 4) p.nt = 2;
+  if (p.wk != 1 && p.wk != 2 && p.wk != 4) p.wk = 1;
+  if (p.ring != 3 && p.ring != 4 && p.ring != 6) p.ring = 4;
+  // A_INSTR >= 1: WK * MP / 16 >= 1 always holds for MP >= 16.
+  while (p.nt > 1 && N % (kWaves / p.wk * p.nt * 16)) p.nt /= 2;
+  while (p.wk < 4 && N % (kWaves / p.wk * p.nt * 16)) p.wk *= 2;
+  p.nblocks = N / (kWaves / p.wk * p.nt * 16);
+  p.splits = max(1, min(p.splits, max(1, NG / (2 * p.wk))));
+  const int ngr = cdiv(NG, p.splits);
+  const int wc = kWaves / p.wk * p.nt * 16;
+  const int sbytes = cdiv(ngr * wc * 2, 256) * 256;
+  while (p.ring > 3 && p.ring * stage_bytes(p.mr, p.nt, p.wk) + sbytes > kDecodeLdsMax) p.ring = p.ring == 6 ? 4 : 3;
+  const int stage = p.ring * stage_bytes(p.mr, p.nt, p.wk) + sbytes;
+  const int red = (p.wk - 1) * (kWaves / p.wk) * p.nt * (p.mr > 16 ? 2 : 1) * 256 * 4;
+  p.lds = stage > red ? stage : red;
+  return p;
+}
+
+size_t decode_ticket_bytes(const DecodePlan& p) {
+  return ((size_t)p.nblocks * p.mchunks * sizeof(int) + 255) & ~(size_t)255;
+}
+
+size_t decode_partial_bytes(const DecodePlan& p, int M, int N) {
+  return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
+}
+
+void launch_decode(const DecodePlan& p, int dtype, const DecodeArgs& x, hipStream_t stream) {
+  if (dtype == TI_DTYPE_F16) launch_mr<TI_DTYPE_F16>(p, x, stream);
+  else launch_mr<TI_DTYPE_BF16>(p, x, stream);
+}
+
+}  // namespace int4
+}  // namespace ti

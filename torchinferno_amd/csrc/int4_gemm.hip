@@ -34,12 +34,11 @@
 // same ring instead.  Wave partials are reduced through LDS in a fixed order;
 // split partials are summed in split order by the last workgroup of the tile
 // (or by a second kernel), so results are deterministic and nothing is memset.
-#include "ti_common.h"
+#include "int4_decode.h"
 
 namespace ti {
 namespace int4 {
 
-constexpr int kGroup = 128;
 constexpr int kLdsBudget = 48 * 1024;  // A + scales staged per workgroup
 
 __device__ __forceinline__ uint32_t interleave_nibbles(uint32_t w) {
@@ -66,54 +65,6 @@ __global__ void repack_weight_kernel(const uint32_t* __restrict__ q, uint32_t* _
   int c = lane & 15, kq = lane >> 4;
   long krow = g * 16 + j * 4 + kq;  // canonical word row: k/8
   out[idx] = interleave_nibbles(q[krow * N + t * 16 + c]);
-}
-
-template <int DT>
-struct Magic;
-template <>
-struct Magic<TI_DTYPE_F16> {
-  static constexpr uint32_t kOr = 0x64006400u;            // 1024 + q
-  static constexpr float kBias = 1032.0f;                 // 1024 + zero point 8
-  static constexpr uint32_t kNegBiasPair = 0xE408E408u;   // fp16 -1032 x2
-};
-template <>
-struct Magic<TI_DTYPE_BF16> {
-  static constexpr uint32_t kOr = 0x43004300u;            // 128 + q
-  static constexpr float kBias = 136.0f;                  // 128 + zero point 8
-  static constexpr uint32_t kNegBiasPair = 0xC308C308u;   // bf16 -136 x2
-};
-
-// (x & mask) | magic in one v_and_or_b32 (the compiler otherwise splits it).
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t magic) {
-  uint32_t r;
-  asm volatile("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(mask), "v"(magic));
-  return r;
-}
-
-template <int DT>
-__device__ __forceinline__ i32x4 unpack8(uint32_t w, uint32_t mask, uint32_t magic) {
-  i32x4 r;
-  r[0] = (int)and_or(w, mask, magic);
-  r[1] = (int)and_or(w >> 4, mask, magic);
-  r[2] = (int)and_or(w >> 8, mask, magic);
-  r[3] = (int)and_or(w >> 12, mask, magic);
-  return r;
-}
-
-template <int DT>
-__device__ __forceinline__ f32x4 mfma16x16x32(i32x4 a, i32x4 b, f32x4 c) {
-  if constexpr (DT == TI_DTYPE_F16) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-}
-
-template <int DT>
-__device__ __forceinline__ float scale_to_f32(uint32_t bits) {
-  return DT == TI_DTYPE_F16 ? f16_bits_to_f32((uint16_t)bits) : bf16_bits_to_f32((uint16_t)bits);
 }
 
 // Exact dequant of the block layout, through the same unpack8: one wave per block.
@@ -161,35 +112,6 @@ __device__ __forceinline__ void load_stage(Stage<MT, NT, ALDS>& st, const i32x4*
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) st.a[mt][j] = *(const i32x4*)(arow[mt] + g * kGroup + j * 32);
-  }
-}
-
-template <int DT, int MT, int NT>
-__device__ __forceinline__ void compute_group(const i32x4 (&w)[NT], const i32x4 (&a)[MT][4],
-                                              const float (&sc)[NT], f32x4 (&acc)[NT][MT]) {
-  const uint32_t mask = 0x000F000Fu, magic = Magic<DT>::kOr;
-  const i32x4 negbias = {(int)Magic<DT>::kNegBiasPair, (int)Magic<DT>::kNegBiasPair,
-                         (int)Magic<DT>::kNegBiasPair, (int)Magic<DT>::kNegBiasPair};
-  f32x4 nbias[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    nbias[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) nbias[mt] = mfma16x16x32<DT>(a[mt][j], negbias, nbias[mt]);
-  }
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    i32x4 b[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = unpack8<DT>((uint32_t)w[t][j], mask, magic);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      f32x4 cc = nbias[mt];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) cc = mfma16x16x32<DT>(a[mt][j], b[j], cc);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[t][mt][i] = __builtin_fmaf(sc[t], cc[i], acc[t][mt][i]);
-    }
   }
 }
 
@@ -253,12 +175,18 @@ __global__ __launch_bounds__(64 * W) void w4a16_gemm_kernel(
 
   // The first D groups of weights go out before the LDS staging, so the
   // staging's latency overlaps theirs.
+  // Every wave runs nit = ceil(n / D) iterations of D groups with
+  // unconditional loads (group index clamped into [0, NG)); a group past wg1
+  // contributes with scale 0.  Unconditional loads keep the in-order vmcnt
+  // bookkeeping exact across the loop back-edge, so the compiler waits for one
+  // ring stage at a time instead of draining the ring every group.
+  const int nwg = max(wg1 - wg0, 0);
+  const int nit = cdiv(nwg, D);
+  const int gclamp = max(min(wg1, NG) - 1, 0);
   Stage<MT, NT, ALDS> ring[D];
-  if (wg0 < wg1) {
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-      load_stage<MT, NT, ALDS>(ring[d], Wp, arow, tile0, T, min(wg0 + d, wg1 - 1), lane);
-  }
+  for (int d = 0; d < D; ++d)
+    load_stage<MT, NT, ALDS>(ring[d], Wp, arow, tile0, T, min(wg0 + d, gclamp), lane);
 
   // ---- stage A rows [m0, m0+rows) x groups [g0, g1) and the scales in LDS ----
   {
@@ -284,30 +212,32 @@ __global__ __launch_bounds__(64 * W) void w4a16_gemm_kernel(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  if (wg0 < wg1) {
-    for (int gr = wg0; gr < wg1; gr += D) {
+  auto step = [&](int it, bool reload) {
 #pragma unroll
-      for (int d = 0; d < D; ++d) {
-        const int g = gr + d;
-        if (g < wg1) {
-          float sc[NT];
+    for (int d = 0; d < D; ++d) {
+      const int g = wg0 + it * D + d;
+      const int gs = min(g, gclamp) - g0;  // staged-scale / A row index (clamped)
+      float sc[NT];
 #pragma unroll
-          for (int t = 0; t < NT; ++t) sc[t] = scale_to_f32<DT>(sS[(g - g0) * NT * 16 + t * 16 + c]);
-          if constexpr (ALDS) {
-            i32x4 a[MT][4];
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-              for (int j = 0; j < 4; ++j) a[mt][j] = *(const i32x4*)(arow[mt] + (g - g0) * kGroup + j * 32);
-            compute_group<DT, MT, NT>(ring[d].w, a, sc, acc);
-          } else {
-            compute_group<DT, MT, NT>(ring[d].w, ring[d].a, sc, acc);
-          }
-          load_stage<MT, NT, ALDS>(ring[d], Wp, arow, tile0, T, min(g + D, wg1 - 1), lane);
-        }
+      for (int t = 0; t < NT; ++t) {
+        const float v = scale_to_f32<DT>(sS[max(gs, 0) * NT * 16 + t * 16 + c]);
+        sc[t] = g < wg1 ? v : 0.f;
       }
+      if constexpr (ALDS) {
+        i32x4 a[MT][4];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) a[mt][j] = *(const i32x4*)(arow[mt] + max(gs, 0) * kGroup + j * 32);
+        compute_group<DT, MT, NT>(ring[d].w, a, sc, acc);
+      } else {
+        compute_group<DT, MT, NT>(ring[d].w, ring[d].a, sc, acc);
+      }
+      if (reload) load_stage<MT, NT, ALDS>(ring[d], Wp, arow, tile0, T, min(g + D, gclamp), lane);
     }
-  }
+  };
+  for (int it = 0; it + 1 < nit; ++it) step(it, true);
+  if (nit > 0) step(nit - 1, false);
 
   // ---- reduce the waves' partial sums through LDS: wave 0 adds waves 1..W-1
   // in order (deterministic).  The staging area is reused. ----
@@ -536,20 +466,52 @@ extern "C" int ti_int4_dequant(const int32_t* packed_weight, const void* packed_
   return TI_OK;
 }
 
+// Kernel choice by M (measured on MI355X at the Llama-3-8B MLP shapes): the
+// register-ring kernel of this file streams best for M <= 16; the LDS-DMA
+// decode kernel (int4_decode.hip) for 17 <= M <= 64; above, this file's kernel
+// again.  TI_ROCM_W4A16_DECODE_MIN_M / _MAX_M override the range (tuning).
+static int env_int(const char* name, int dflt) {
+  const char* e = getenv(name);
+  return (e && *e) ? atoi(e) : dflt;
+}
+
+static bool use_decode(int M) {
+  return M >= env_int("TI_ROCM_W4A16_DECODE_MIN_M", 17) && M <= env_int("TI_ROCM_W4A16_DECODE_MAX_M", 64);
+}
+
+// Workspace of one call: fp32 partials [splits][M][N] from the start, ticket
+// ints at the 256-aligned end of the caller's buffer.  A buffer of at least
+// max(partial bytes) + max(ticket bytes) + 256 over every problem it serves
+// (ti_w4a16_workspace_bytes_max) never lets one call's partials overlap another
+// call's tickets, which must stay zero between calls.
+struct WsNeed {
+  size_t partial, tickets;
+};
+
+static WsNeed ws_need(int M, int N, int K) {
+  if (use_decode(M)) {
+    DecodePlan d = make_decode_plan(M, N, K);
+    if (d.splits <= 1) return {0, 0};
+    return {decode_partial_bytes(d, M, N), decode_ticket_bytes(d)};
+  }
+  Plan p = make_plan(M, N, K);
+  if (p.splits <= 1) return {0, 0};
+  return {partial_bytes(p, M, N), ticket_bytes(p)};
+}
+
 extern "C" size_t ti_w4a16_workspace_bytes(int M, int N, int K, int group_size) {
   if (M <= 0 || N <= 0 || K <= 0 || group_size != kGroup || N % 64 || K % kGroup) return 0;
-  Plan p = make_plan(M, N, K);
-  return workspace_bytes(p, M, N);
+  WsNeed w = ws_need(M, N, K);
+  return w.partial ? w.partial + w.tickets + 256 : 0;
 }
 
 extern "C" size_t ti_w4a16_workspace_bytes_max(int max_m, int N, int K, int group_size) {
   if (max_m <= 0 || N <= 0 || K <= 0 || group_size != kGroup || N % 64 || K % kGroup) return 0;
   size_t pmax = 0, tmax = 0;
   for (int m = 1; m <= max_m; ++m) {
-    Plan p = make_plan(m, N, K);
-    if (p.splits <= 1) continue;
-    pmax = partial_bytes(p, m, N) > pmax ? partial_bytes(p, m, N) : pmax;
-    tmax = ticket_bytes(p) > tmax ? ticket_bytes(p) : tmax;
+    WsNeed w = ws_need(m, N, K);
+    pmax = w.partial > pmax ? w.partial : pmax;
+    tmax = w.tickets > tmax ? w.tickets : tmax;
   }
   return pmax ? pmax + tmax + 256 : 0;
 }
@@ -628,8 +590,28 @@ extern "C" int ti_w4a16_gemm(const void* a, int dtype, const int32_t* packed_wei
                ((uintptr_t)packed_scales & 15) == 0,
                "ti_w4a16_gemm: a, packed_weight and packed_scales must be 16-byte aligned");
   TI_CHECK_ARG(((uintptr_t)out & 7) == 0, "ti_w4a16_gemm: out must be 8-byte aligned");
+  if (use_decode(M)) {
+    DecodePlan d = make_decode_plan(M, N, K);
+    TI_CHECK_SHAPE(d.lds <= kDecodeLdsMax, "ti_w4a16_gemm: decode plan needs %d bytes of LDS", d.lds);
+    DecodeArgs x{(const uint16_t*)a, (const i32x4*)packed_weight, (const uint16_t*)packed_scales,
+                 (uint16_t*)out, nullptr, nullptr, M, N, K};
+    if (d.splits > 1) {
+      const size_t need = decode_partial_bytes(d, M, N) + decode_ticket_bytes(d) + 256;
+      if (!workspace || workspace_bytes_ < need) {
+        set_error("ti_w4a16_gemm: workspace of %zu bytes required (got %zu)", need, workspace_bytes_);
+        return TI_ERR_WORKSPACE;
+      }
+      TI_CHECK_ARG(((uintptr_t)workspace & 15) == 0, "ti_w4a16_gemm: workspace must be 16-byte aligned");
+      x.partial = (float*)workspace;
+      const uintptr_t end = ((uintptr_t)workspace + workspace_bytes_) & ~(uintptr_t)255;
+      x.tickets = (int*)(end - decode_ticket_bytes(d));
+    }
+    launch_decode(d, dtype, x, stream);
+    TI_CHECK_LAUNCH("ti_w4a16_gemm");
+    return TI_OK;
+  }
   Plan p = make_plan(M, N, K);
-  TI_CHECK_SHAPE(p.lds <= 64 * 1024, "ti_w4a16_gemm: plan needs %d bytes of LDS", p.lds);
+  TI_CHECK_SHAPE(p.lds <= 160 * 1024, "ti_w4a16_gemm: plan needs %d bytes of LDS", p.lds);
   size_t need = workspace_bytes(p, M, N);
   LaunchArgs x{(const uint16_t*)a, (const i32x4*)packed_weight, (const uint16_t*)packed_scales,
                (uint16_t*)out, nullptr, nullptr, M, N, K};
