@@ -86,6 +86,66 @@ int ti_w4a16_gemm(const void* a, int dtype, const int32_t* packed_weight,
                   const void* packed_scales, void* out, int M, int N, int K, int group_size,
                   void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * FP8 e4m3 (OCP float8_e4m3fn) quantizers.  fp32 arithmetic with IEEE
+ * division, round-to-nearest-even cast: codes and scales are bit-identical to
+ * the reference formulas evaluated by torch.
+ * ------------------------------------------------------------------------- */
+
+/* Per-row dynamic quant: xs[m] = max(amax_k |x[m,k]| / 448, eps),
+ * xq[m,k] = e4m3(x[m,k] / xs[m]).  Replaces the per-token activation quant
+ * (Triton _row_scale_cast_fp8 / sgl_per_token_quant_fp8,
+ * src/torchinferno/kernels/fp8.py:53-72,99-116,234-238; eps 1e-10) and, run
+ * over a weight's rows, quantize_weight_fp8_per_channel (fp8.py:129-138).
+ * x fp16/bf16 [M,K] 16-byte aligned, K % 8 == 0; xq [M,K]; xs [M]. */
+int ti_fp8_quant_per_token(const void* x, int x_dtype, int M, int K, float eps,
+                           uint8_t* xq, float* xs, hipStream_t stream);
+
+/* 1 x block_size activation quant (block_size == 128): per (row, block)
+ * s = max(amax, 1e-4) * (1/448) -- or 2^ceil(log2(that)) if round_scale --
+ * xq = e4m3(clamp(x / s, -448, 448)).  Replaces act_quant
+ * (src/torchinferno/kernels/deepseek_v4_tilelang.py:147-173, kernel
+ * deepseek_v4_tilelang_definitions.py:273-331).  xs [M, K/128]. */
+int ti_fp8_quant_block(const void* x, int x_dtype, int M, int K, int block_size,
+                       int round_scale, uint8_t* xq, float* xs, hipStream_t stream);
+
+/* Tensor-scale cast xq = e4m3(x * inv_scale[0]) over n elements (n % 8 == 0).
+ * Replaces the Triton _scale_cast_fp8 of quantize_activation_fp8
+ * (src/torchinferno/kernels/fp8.py:43-51,141-181). */
+int ti_fp8_quant_tensor(const void* x, int x_dtype, long n, const float* inv_scale,
+                        uint8_t* xq, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * FP8 W8A8 GEMMs: out[M,N] = a[M,K] . b[N,K]^T (both e4m3, K-contiguous, the
+ * "b = weight.t(), column-major" layout of torch._scaled_mm), fp32
+ * accumulation, out bf16 or fp16.  Requires K % 128 == 0; M, N arbitrary.
+ * Skinny M may split K across workgroups: pass a workspace of
+ * ti_fp8_gemm_workspace_bytes() (zero-filled once when allocated; every call
+ * leaves its ticket words zero again; calls sharing one workspace must be
+ * stream-ordered).  scale_mode: 0 = row/column scales, 1 = 128x128 blocks.
+ * ------------------------------------------------------------------------- */
+size_t ti_fp8_gemm_workspace_bytes(int M, int N, int K, int scale_mode);
+size_t ti_fp8_gemm_workspace_bytes_max(int max_m, int N, int K, int scale_mode);
+
+/* out = (a . b^T) * a_scale[m] * b_scale[n]; a_scale_per_row / b_scale_per_col
+ * = 0 broadcast a single scale (tensorwise).  Replaces torch._scaled_mm /
+ * aten::_scaled_mm.out as called by fp8_prefill_linear and
+ * fp8_per_token_linear_quantized (src/torchinferno/kernels/fp8.py:184-327),
+ * sgl fp8_scaled_mm, and torchinferno_sgl_fp8::scaled_mm_out
+ * (src/torchinferno/kernels/csrc/sgl_fp8_out.cpp:17-83, no M <= 64 limit). */
+int ti_fp8_gemm_rowcol(const uint8_t* a, const float* a_scale, int a_scale_per_row,
+                       const uint8_t* b, const float* b_scale, int b_scale_per_col,
+                       void* out, int out_dtype, int M, int N, int K,
+                       void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Block-scaled: out[m,n] = sum_kb (a . b^T over K block kb) * a_scale[m,kb] *
+ * b_scale[n/128, kb]; a_scale [M, K/128], b_scale [ceil(N/128), K/128], fp32.
+ * Replaces fp8_gemm (src/torchinferno/kernels/deepseek_v4_tilelang.py:207-223,
+ * kernel deepseek_v4_tilelang_definitions.py:436-485). */
+int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, const uint8_t* b,
+                      const float* b_scale, void* out, int out_dtype, int M, int N, int K,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,489 @@
+// FP8 e4m3 W8A8 GEMM for gfx950: C[M,N] = A[M,K] . B[N,K]^T with
+//   * row/column scales  (SMODE 0): C = acc * sa[m] * sb[n]; sa/sb may also be
+//     scalars -- the per-token x per-channel and tensorwise linears of
+//     src/torchinferno/kernels/fp8.py:184-327 (torch._scaled_mm, sgl cutlass,
+//     src/torchinferno/kernels/csrc/sgl_fp8_out.cpp:17-83);
+//   * 128x128 block scales (SMODE 1): every 128-wide K block's partial sum is
+//     scaled by sa[m, kb] * sb[n / 128, kb] and added into an fp32
+//     accumulator -- DeepSeek fp8_gemm,
+//     src/torchinferno/kernels/deepseek_v4_tilelang_definitions.py:436-485.
+// A and B are K-contiguous e4m3 (OCP float8_e4m3fn, gfx950's native FP8).
+//
+// Structure.  A workgroup owns a BM x BN output tile and walks K in steps of
+// 128 bytes.  Each step's A and B slabs (BM and BN rows of 128 B) reach LDS by
+// direct DMA (global_load_lds_dwordx4, issued from inline asm with explicit
+// vmcnt accounting) through a ring of R stages; block mode also DMAs the
+// step's BM activation scales.  Rows are stored with their eight 16-byte
+// chunks XOR-swizzled (chunk c of row r at position c ^ ((r >> 1) & 7)): the
+// DMA side reads whole 128 B row segments (coalesced), and the MFMA operand
+// reads -- 16 lanes on 16 consecutive rows, same chunk -- hit 16 distinct
+// bank groups.  Waves form a WGM x WGN grid over the tile; each runs
+// v_mfma_scale_f32_{32x32x64,16x16x128}_f8f6f4 with unit scales (e8m0 127).
+// Both operands give lane l row (l % MF) and the same 32 K bytes, so every
+// MFMA k-slot pairs A and B at one true k.
+//
+// Split-K (SPLIT 2, skinny M): `splits` workgroups share a tile; each writes
+// an fp32 partial with agent-scope stores, takes a ticket, and the last one
+// sums the partials in split order (deterministic) and stores C.
+//
+// Tile order: WG t is dispatched to XCD t % 8; t is remapped so that each XCD
+// works through one contiguous run of a GM-row grouped raster, keeping the A
+// and B slabs its L2 holds shared by the tiles in flight there.
+#include "fp8_common.h"
+#include "fp8_gemm.h"
+#include "lds_dma.h"
+
+namespace ti {
+namespace fp8 {
+namespace {
+
+template <int MF>
+struct Mfma;
+
+template <>
+struct Mfma<32> {
+  typedef f32x16 acc_t;
+  static constexpr int KS = 2;   // MFMAs per 128-byte K step
+  static constexpr int NACC = 16;
+  static __device__ __forceinline__ acc_t mma(i32x8 a, i32x8 b, acc_t c) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+  }
+  // Row (within the 32x32 tile) of accumulator element e of this lane.
+  static __device__ __forceinline__ int row(int e, int lane) { return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3); }
+  // First of the two 16-byte chunks (of the 128-byte K step) lane reads for MFMA ks.
+  static __device__ __forceinline__ int chunk(int ks, int lane) { return ks * 4 + (lane >> 5) * 2; }
+};
+
+template <>
+struct Mfma<16> {
+  typedef f32x4 acc_t;
+  static constexpr int KS = 1;
+  static constexpr int NACC = 4;
+  static __device__ __forceinline__ acc_t mma(i32x8 a, i32x8 b, acc_t c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+  }
+  static __device__ __forceinline__ int row(int e, int lane) { return 4 * (lane >> 4) + e; }
+  static __device__ __forceinline__ int chunk(int, int lane) { return (lane >> 4) * 2; }
+};
+
+// Byte offset of 16-byte chunk c of row r in a swizzled [rows x 128 B] slab.
+__device__ __forceinline__ int swz(int r, int c) { return (r * 8 + (c ^ ((r >> 1) & 7))) * 16; }
+
+template <int ODT>
+__device__ __forceinline__ uint16_t out_bits(float v) {
+  if constexpr (ODT == TI_DTYPE_F16) return f32_to_f16_bits(v);
+  else return f32_to_bf16_bits(v);
+}
+
+template <int BM, int BN, int WGM, int WGN, int MF, int R, int SMODE, int SPLIT, int ODT>
+__global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
+  using MM = Mfma<MF>;
+  typedef typename MM::acc_t acc_t;
+  constexpr int W = WGM * WGN;
+  constexpr int TM = BM / WGM, TN = BN / WGN;
+  constexpr int FM = TM / MF, FN = TN / MF;
+  static_assert(FM >= 1 && FN >= 1 && TM % MF == 0 && TN % MF == 0, "wave tile must hold whole MFMA tiles");
+  static_assert(SMODE == 0 || 128 % TN == 0, "block scales need a wave's columns inside one 128 block");
+  constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
+  // Block mode also stages the step's BM activation scales and (one 256-byte
+  // DMA) the weight scales of the tile's 128-column blocks.
+  constexpr int SA_BYTES = SMODE == 1 ? ((BM * 4 + 255) / 256) * 256 + 256 : 0;
+  constexpr int STAGE = A_BYTES + B_BYTES + SA_BYTES;
+  constexpr int NI_AB = (A_BYTES + B_BYTES) / 1024;
+  constexpr int NI_SA = SMODE == 1 ? SA_BYTES / 256 - 1 : 0;
+  constexpr int NI = NI_AB + (SMODE == 1 ? NI_SA + 1 : 0);  // DMAs per stage, all waves
+  constexpr int NI_LO = NI / W, NI_HI = (NI + W - 1) / W;
+  constexpr int P = R - 1;
+  static_assert(R >= 2, "ring needs two stages");
+  static_assert(NI_HI * (P > 1 ? P - 1 : 1) <= 63, "vmcnt holds at most 63 outstanding loads");
+
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ int last_flag;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int M = x.M, N = x.N, K = x.K;
+  const int KT = K / 128;
+
+  // ---- tile of this workgroup (XCD-contiguous runs of a grouped raster) ----
+  int t = blockIdx.x;
+  const int nt = gridDim.x;
+  if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);
+  const int tiles_m = x.tiles_m, tiles_n = x.tiles_n;
+  constexpr int GM = 8;
+  const int group = t / (GM * tiles_n);
+  const int first_m = group * GM;
+  const int gsz = min(tiles_m - first_m, GM);
+  const int tin = t - group * GM * tiles_n;
+  const int tm = first_m + tin % gsz, tn = tin / gsz;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int split = blockIdx.y;
+  const int per = cdiv(KT, x.splits);
+  const int ks0 = split * per;
+  const int nsteps = max(min(KT, ks0 + per) - ks0, 0);
+
+  const uint32_t ring0 = lds_offset(smem);
+  const int n_mine = (NI - wave + W - 1) / W;  // DMAs of this wave per stage
+
+  auto issue = [&](int i) {
+    const uint32_t base = ring0 + (uint32_t)((i % R) * STAGE);
+    const long kk = ks0 + i;
+#pragma unroll
+    for (int u = 0; u < NI_HI; ++u) {
+      const int id = wave + u * W;
+      if (id >= NI) break;
+      if (id < NI_AB) {
+        const bool is_a = id < A_BYTES / 1024;
+        const int j = is_a ? id : id - A_BYTES / 1024;
+        const int r = 8 * j + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        const uint8_t* src = is_a ? x.a + (long)min(m0 + r, M - 1) * K
+                                  : x.b + (long)min(n0 + r, N - 1) * K;
+        dma16(src + kk * 128 + c * 16, base + (uint32_t)((is_a ? 0 : A_BYTES) + j * 1024));
+      } else if (id < NI_AB + NI_SA) {
+        const int j = id - NI_AB;
+        const int e = j * 64 + lane;
+        const int row = min(m0 + min(e, BM - 1), M - 1);
+        dma4(x.sa + (long)row * KT + kk, base + (uint32_t)(A_BYTES + B_BYTES + j * 256));
+      } else {
+        const int nb = min(n0 / 128 + lane, (N + 127) / 128 - 1);
+        dma4(x.sb + (long)nb * KT + kk, base + (uint32_t)(A_BYTES + B_BYTES + NI_SA * 256));
+      }
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < P; ++s)
+    if (s < nsteps) issue(s);
+
+  acc_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < MM::NACC; ++e) acc[i][j][e] = 0.f;
+
+  const int arow0 = wm * TM + (lane % MF);
+  const int brow0 = wn * TN + (lane % MF);
+
+  for (int i = 0; i < nsteps; ++i) {
+    if (i + P - 1 < nsteps) {
+      if constexpr (P > 1) {
+        if (n_mine > NI_LO) wait_vm_barrier<(P - 1) * NI_HI>();
+        else wait_vm_barrier<(P - 1) * NI_LO>();
+      } else {
+        wait_vm_barrier<0>();
+      }
+    } else {
+      wait_vm_barrier<0>();
+    }
+    if (i + P < nsteps) issue(i + P);
+
+    const uint8_t* st = smem + (i % R) * STAGE;
+    const uint8_t* sA = st;
+    const uint8_t* sB = st + A_BYTES;
+    if constexpr (SMODE == 0) {
+#pragma unroll
+      for (int ks = 0; ks < MM::KS; ++ks) {
+        const int c0 = MM::chunk(ks, lane);
+        i32x8 af[FM], bf[FN];
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+          const int r = arow0 + fm * MF;
+          const i32x4 lo = *(const i32x4*)(sA + swz(r, c0));
+          const i32x4 hi = *(const i32x4*)(sA + swz(r, c0 + 1));
+          af[fm] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const int r = brow0 + fn * MF;
+          const i32x4 lo = *(const i32x4*)(sB + swz(r, c0));
+          const i32x4 hi = *(const i32x4*)(sB + swz(r, c0 + 1));
+          bf[fn] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = MM::mma(af[fm], bf[fn], acc[fm][fn]);
+      }
+    } else {
+      const float* sS = (const float*)(st + A_BYTES + B_BYTES);
+      const float sbv = sS[NI_SA * 64 + (wn * TN) / 128];
+      // All B fragments of the step stay in registers; A is read one M tile
+      // at a time (bounds register use with the per-tile partial sums).
+      i32x8 bf[MM::KS][FN];
+#pragma unroll
+      for (int ks = 0; ks < MM::KS; ++ks) {
+        const int c0 = MM::chunk(ks, lane);
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const int r = brow0 + fn * MF;
+          const i32x4 lo = *(const i32x4*)(sB + swz(r, c0));
+          const i32x4 hi = *(const i32x4*)(sB + swz(r, c0 + 1));
+          bf[ks][fn] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+      }
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        i32x8 af[MM::KS];
+        const int r = arow0 + fm * MF;
+#pragma unroll
+        for (int ks = 0; ks < MM::KS; ++ks) {
+          const int c0 = MM::chunk(ks, lane);
+          const i32x4 lo = *(const i32x4*)(sA + swz(r, c0));
+          const i32x4 hi = *(const i32x4*)(sA + swz(r, c0 + 1));
+          af[ks] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+        float srow[MM::NACC];
+#pragma unroll
+        for (int e = 0; e < MM::NACC; ++e) srow[e] = sS[wm * TM + fm * MF + MM::row(e, lane)] * sbv;
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          acc_t p;
+#pragma unroll
+          for (int e = 0; e < MM::NACC; ++e) p[e] = 0.f;
+#pragma unroll
+          for (int ks = 0; ks < MM::KS; ++ks) p = MM::mma(af[ks], bf[ks][fn], p);
+#pragma unroll
+          for (int e = 0; e < MM::NACC; ++e) acc[fm][fn][e] = __builtin_fmaf(p[e], srow[e], acc[fm][fn][e]);
+        }
+      }
+    }
+  }
+  wait_vm_all();
+
+  // ---- epilogue ----
+  const int col_l = lane % MF;
+  if constexpr (SPLIT == 0) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const int col = n0 + wn * TN + fn * MF + col_l;
+        float sbn = 1.f;
+        if constexpr (SMODE == 0) sbn = col < N ? x.sb[(long)col * x.sb_stride] : 0.f;
+#pragma unroll
+        for (int e = 0; e < MM::NACC; ++e) {
+          const int row = m0 + wm * TM + fm * MF + MM::row(e, lane);
+          if (row < M && col < N) {
+            float v = acc[fm][fn][e];
+            if constexpr (SMODE == 0) v = v * x.sa[(long)row * x.sa_stride] * sbn;
+            x.out[(long)row * N + col] = out_bits<ODT>(v);
+          }
+        }
+      }
+    return;
+  } else {
+    const long mn = (long)M * N;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const int col = n0 + wn * TN + fn * MF + col_l;
+#pragma unroll
+        for (int e = 0; e < MM::NACC; ++e) {
+          const int row = m0 + wm * TM + fm * MF + MM::row(e, lane);
+          if (row < M && col < N)
+            __hip_atomic_store(&x.partial[split * mn + (long)row * N + col], acc[fm][fn][e],
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int* ticket = x.tickets + blockIdx.x;
+    if (threadIdx.x == 0)
+      last_flag = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == x.splits - 1;
+    __syncthreads();
+    if (!last_flag) return;
+    const int rows = min(BM, M - m0), cols = min(BN, N - n0);
+    for (int e = threadIdx.x; e < rows * cols; e += 64 * W) {
+      const int row = m0 + e / cols, col = n0 + e % cols;
+      const long off = (long)row * N + col;
+      float v = 0.f;
+      for (int sp = 0; sp < x.splits; ++sp)
+        v += __hip_atomic_load(&x.partial[sp * mn + off], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if constexpr (SMODE == 0) v = v * x.sa[(long)row * x.sa_stride] * x.sb[(long)col * x.sb_stride];
+      x.out[off] = out_bits<ODT>(v);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tile configurations (kind):
+//   0  BM=256 BN=256, 8 waves 2x4 (wave 128x64), 32x32 MFMA, 2 stages  -- prefill
+//   1  BM=256 BN=256, 4 waves 2x2 (wave 128x128), 32x32 MFMA, 2 stages -- prefill
+//   2  BM=128 BN=128, 4 waves 2x2 (wave 64x64),  32x32 MFMA, 3 stages -- mid M
+//   3  BM=16  BN=256, 4 waves 1x4 (wave 16x64),  16x16 MFMA, 4 stages -- decode
+//   4  BM=32  BN=256, 4 waves 1x4 (wave 32x64),  16x16 MFMA, 4 stages -- decode
+//   5  BM=64  BN=128, 4 waves 1x4 (wave 64x32),  16x16 MFMA, 4 stages -- small M
+//   6  BM=16  BN=128, 4 waves 1x4 (wave 16x32),  16x16 MFMA, 6 stages -- decode
+template <int BM, int BN, int WGM, int WGN, int MF, int R, int SMODE>
+constexpr int cfg_lds() {
+  return R * (BM * 128 + BN * 128 + (SMODE == 1 ? ((BM * 4 + 255) / 256) * 256 + 256 : 0));
+}
+
+template <int BM, int BN, int WGM, int WGN, int MF, int R, int SMODE, int ODT>
+void launch_cfg(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
+  constexpr int lds = cfg_lds<BM, BN, WGM, WGN, MF, R, SMODE>();
+  dim3 grid(p.tiles_m * p.tiles_n, p.splits);
+  if (p.splits > 1)
+    hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, WGM, WGN, MF, R, SMODE, 2, ODT>), grid, dim3(64 * WGM * WGN),
+                       lds, stream, x);
+  else
+    hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, WGM, WGN, MF, R, SMODE, 0, ODT>), grid, dim3(64 * WGM * WGN),
+                       lds, stream, x);
+}
+
+template <int SMODE, int ODT>
+void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
+  switch (p.kind) {
+    case 0: launch_cfg<256, 256, 2, 4, 32, 2, SMODE, ODT>(p, x, stream); break;
+    case 1: launch_cfg<256, 256, 2, 2, 32, 2, SMODE, ODT>(p, x, stream); break;
+    case 2: launch_cfg<128, 128, 2, 2, 32, 3, SMODE, ODT>(p, x, stream); break;
+    case 3: launch_cfg<16, 256, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
+    case 4: launch_cfg<32, 256, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
+    case 5: launch_cfg<64, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
+    default: launch_cfg<16, 128, 1, 4, 16, 6, SMODE, ODT>(p, x, stream); break;
+  }
+}
+
+const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16};
+const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128};
+
+int env_int(const char* name, int dflt) {
+  const char* e = getenv(name);
+  return (e && *e) ? atoi(e) : dflt;
+}
+
+}  // namespace
+
+GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
+  GemmPlan p;
+  const int KT = K / 128;
+  // Heuristic (MI355X, 256 CUs): skinny M streams B with a 16/32-row tile and
+  // split-K up to ~2 workgroups per CU; large M uses 256x256 tiles, 128x128
+  // when 256x256 leaves the chip under-filled.
+  if (M <= 16) p.kind = N >= 16384 ? 6 : 3;
+  else if (M <= 32) p.kind = 4;
+  else if (M <= 128) p.kind = 5;
+  else {
+    const long big = (long)cdiv(M, 256) * cdiv(N, 256);
+    p.kind = big >= 192 ? 0 : 2;
+  }
+  p.kind = env_int("TI_ROCM_FP8_KIND", p.kind);
+  if (p.kind < 0 || p.kind >= kNumKinds) p.kind = 0;
+  p.tiles_m = cdiv(M, kBM[p.kind]);
+  p.tiles_n = cdiv(N, kBN[p.kind]);
+  const long tiles = (long)p.tiles_m * p.tiles_n;
+  int splits = 1;
+  if (tiles < 256) {
+    splits = cdiv(512, (int)tiles);
+    const int cap = KT / 8 > 1 ? KT / 8 : 1;  // at least 8 K steps per split
+    splits = splits < cap ? splits : cap;
+  }
+  splits = env_int("TI_ROCM_FP8_SPLITS", splits);
+  p.splits = splits < 1 ? 1 : (splits > KT ? KT : splits);
+  (void)smode;
+  return p;
+}
+
+size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
+  if (p.splits <= 1) return 0;
+  const size_t part = (size_t)p.splits * M * N * sizeof(float);
+  const size_t tick = ((size_t)p.tiles_m * p.tiles_n * sizeof(int) + 255) & ~(size_t)255;
+  return part + tick + 256;
+}
+
+size_t gemm_ticket_bytes(const GemmPlan& p) {
+  return ((size_t)p.tiles_m * p.tiles_n * sizeof(int) + 255) & ~(size_t)255;
+}
+
+void launch_gemm(const GemmPlan& p, int smode, int odt, const GemmArgs& x, hipStream_t stream) {
+  if (smode == 0) {
+    if (odt == TI_DTYPE_F16) launch_kind<0, TI_DTYPE_F16>(p, x, stream);
+    else launch_kind<0, TI_DTYPE_BF16>(p, x, stream);
+  } else {
+    if (odt == TI_DTYPE_F16) launch_kind<1, TI_DTYPE_F16>(p, x, stream);
+    else launch_kind<1, TI_DTYPE_BF16>(p, x, stream);
+  }
+}
+
+}  // namespace fp8
+}  // namespace ti
+
+using namespace ti;
+using namespace ti::fp8;
+
+static int gemm_common(const char* name, int smode, const uint8_t* a, const float* a_scale,
+                       int a_scale_stride, const uint8_t* b, const float* b_scale, int b_scale_stride,
+                       void* out, int out_dtype, int M, int N, int K, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
+  TI_CHECK_ARG(a && b && a_scale && b_scale && out, "%s: null pointer", name);
+  TI_CHECK_ARG(out_dtype == TI_DTYPE_BF16 || out_dtype == TI_DTYPE_F16, "%s: out dtype must be bf16 or fp16",
+               name);
+  TI_CHECK_SHAPE(M >= 0 && N > 0 && K > 0 && K % 128 == 0, "%s: need K %% 128 == 0 (M=%d N=%d K=%d)", name,
+                 M, N, K);
+  TI_CHECK_ARG(((uintptr_t)a & 15) == 0 && ((uintptr_t)b & 15) == 0, "%s: a and b must be 16-byte aligned",
+               name);
+  TI_CHECK_ARG(((uintptr_t)out & 1) == 0 && ((uintptr_t)a_scale & 3) == 0 && ((uintptr_t)b_scale & 3) == 0,
+               "%s: misaligned out or scales", name);
+  if (M == 0) return TI_OK;
+  GemmPlan p = make_gemm_plan(M, N, K, smode);
+  GemmArgs x{};
+  x.a = a; x.b = b; x.sa = a_scale; x.sb = b_scale;
+  x.sa_stride = a_scale_stride; x.sb_stride = b_scale_stride;
+  x.out = (uint16_t*)out;
+  x.M = M; x.N = N; x.K = K;
+  x.splits = p.splits; x.tiles_m = p.tiles_m; x.tiles_n = p.tiles_n;
+  const size_t need = gemm_workspace_bytes(p, M, N);
+  if (need) {
+    if (!workspace || workspace_bytes < need) {
+      set_error("%s: workspace of %zu bytes required (got %zu)", name, need, workspace_bytes);
+      return TI_ERR_WORKSPACE;
+    }
+    TI_CHECK_ARG(((uintptr_t)workspace & 15) == 0, "%s: workspace must be 16-byte aligned", name);
+    x.partial = (float*)workspace;
+    const uintptr_t end = ((uintptr_t)workspace + workspace_bytes) & ~(uintptr_t)255;
+    x.tickets = (int*)(end - gemm_ticket_bytes(p));
+  }
+  launch_gemm(p, smode, out_dtype, x, stream);
+  TI_CHECK_LAUNCH(name);
+  return TI_OK;
+}
+
+extern "C" size_t ti_fp8_gemm_workspace_bytes(int M, int N, int K, int scale_mode) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 128) return 0;
+  return gemm_workspace_bytes(make_gemm_plan(M, N, K, scale_mode), M, N);
+}
+
+extern "C" size_t ti_fp8_gemm_workspace_bytes_max(int max_m, int N, int K, int scale_mode) {
+  if (max_m <= 0 || N <= 0 || K <= 0 || K % 128) return 0;
+  size_t pmax = 0, tmax = 0;
+  for (int m = 1; m <= max_m; ++m) {
+    GemmPlan p = make_gemm_plan(m, N, K, scale_mode);
+    if (p.splits <= 1) continue;
+    const size_t part = (size_t)p.splits * m * N * sizeof(float);
+    pmax = part > pmax ? part : pmax;
+    tmax = gemm_ticket_bytes(p) > tmax ? gemm_ticket_bytes(p) : tmax;
+  }
+  return pmax ? pmax + tmax + 256 : 0;
+}
+
+extern "C" int ti_fp8_gemm_rowcol(const uint8_t* a, const float* a_scale, int a_scale_per_row,
+                                  const uint8_t* b, const float* b_scale, int b_scale_per_col, void* out,
+                                  int out_dtype, int M, int N, int K, void* workspace, size_t workspace_bytes,
+                                  hipStream_t stream) {
+  return gemm_common("ti_fp8_gemm_rowcol", 0, a, a_scale, a_scale_per_row ? 1 : 0, b, b_scale,
+                     b_scale_per_col ? 1 : 0, out, out_dtype, M, N, K, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, const uint8_t* b,
+                                 const float* b_scale, void* out, int out_dtype, int M, int N, int K,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return gemm_common("ti_fp8_gemm_block", 1, a, a_scale, 0, b, b_scale, 0, out, out_dtype, M, N, K, workspace,
+                     workspace_bytes, stream);
+}

@@ -1,0 +1,196 @@
+// FP8 e4m3 activation quantizers for gfx950.
+//
+//   per-token (one scale per row; also the per-output-channel weight quant,
+//     which is the same formula over a weight's rows):
+//     s[m] = max(amax_k |x[m,k]| / 448, eps), q = e4m3(x / s)
+//     -- src/torchinferno/kernels/fp8.py:53-72 (Triton _row_scale_cast_fp8),
+//        fp8.py:129-138 (quantize_weight_fp8_per_channel, eps 1e-10)
+//   1x128 block (DeepSeek act_quant):
+//     s = max(amax_blk, 1e-4) * (1/448)  [or 2^ceil(log2(amax*(1/448)))],
+//     q = e4m3(clamp(x / s, -448, 448))
+//     -- src/torchinferno/kernels/deepseek_v4_tilelang_definitions.py:255-331
+//   tensor scale (static or precomputed dynamic scale):
+//     q = e4m3(x * inv_scale)  -- fp8.py:43-51 (_scale_cast_fp8)
+//
+// All arithmetic is fp32 with IEEE division (no reciprocal approximation), and
+// the cast is round-to-nearest-even, so codes and scales are bit-identical to
+// the same formulas evaluated by torch on the host.
+#include "fp8_common.h"
+
+namespace ti {
+namespace fp8 {
+namespace {
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+template <int DT>
+__device__ __forceinline__ void load8(const uint16_t* p, float (&f)[8]) {
+  const uint4 v = *(const uint4*)p;
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = act_to_f32<DT>((uint16_t)(w[i] & 0xFFFFu));
+    f[2 * i + 1] = act_to_f32<DT>((uint16_t)(w[i] >> 16));
+  }
+}
+
+__device__ __forceinline__ uint2 pack8(const uint32_t (&c)[8]) {
+  return make_uint2(c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24),
+                    c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24));
+}
+
+// One workgroup (256 threads) per row; K % 8 == 0.
+template <int DT>
+__global__ __launch_bounds__(256) void quant_per_token_kernel(const uint16_t* __restrict__ x, int K,
+                                                              uint8_t* __restrict__ q,
+                                                              float* __restrict__ s, float eps) {
+  __shared__ float red[4];
+  const long row = blockIdx.x;
+  const uint16_t* xr = x + row * K;
+  float amax = 0.f;
+  for (int i = threadIdx.x * 8; i < K; i += 256 * 8) {
+    float f[8];
+    load8<DT>(xr + i, f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
+  }
+  amax = wave_max(amax);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float sc = fmaxf(amax / kE4M3Max, eps);
+  if (threadIdx.x == 0) s[row] = sc;
+  uint8_t* qr = q + row * K;
+  for (int i = threadIdx.x * 8; i < K; i += 256 * 8) {
+    float f[8];
+    load8<DT>(xr + i, f);
+    uint32_t c[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c[e] = e4m3_encode(f[e] / sc);
+    *(uint2*)(qr + i) = pack8(c);
+  }
+}
+
+// One wave per (row, 128-column block): 2 elements per lane.
+template <int DT, bool POW2>
+__global__ __launch_bounds__(256) void quant_block_kernel(const uint16_t* __restrict__ x, int M, int K,
+                                                          uint8_t* __restrict__ q,
+                                                          float* __restrict__ s) {
+  const int lane = threadIdx.x & 63;
+  const int KB = K / 128;
+  const long blk = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= (long)M * KB) return;
+  const long row = blk / KB;
+  const int kb = (int)(blk % KB);
+  const long off = row * K + (long)kb * 128 + lane * 2;
+  const uint32_t w = *(const uint32_t*)(x + off);
+  const float f0 = act_to_f32<DT>((uint16_t)(w & 0xFFFFu));
+  const float f1 = act_to_f32<DT>((uint16_t)(w >> 16));
+  float amax = wave_max(fmaxf(fabsf(f0), fabsf(f1)));
+  amax = fmaxf(amax, 1e-4f);
+  const float inv_max = 1.0f / kE4M3Max;  // fp32 constant, as the reference's fp8_max_inv
+  float sc;
+  if constexpr (POW2) {
+    // 2^ceil(log2(amax / 448)) from the exponent and mantissa bits.
+    const uint32_t b = __float_as_uint(amax * inv_max);
+    const int e = (int)((b >> 23) & 0xFF) - 127 + ((b & 0x7FFFFFu) != 0 ? 1 : 0);
+    sc = __uint_as_float((uint32_t)(e + 127) << 23);
+  } else {
+    sc = amax * inv_max;
+  }
+  const float y0 = fminf(fmaxf(f0 / sc, -kE4M3Max), kE4M3Max);
+  const float y1 = fminf(fmaxf(f1 / sc, -kE4M3Max), kE4M3Max);
+  *(uint16_t*)(q + off) = (uint16_t)(e4m3_encode(y0) | (e4m3_encode(y1) << 8));
+  if (lane == 0) s[row * KB + kb] = sc;
+}
+
+// q = e4m3(x * inv_scale[0]); n % 8 == 0.
+template <int DT>
+__global__ __launch_bounds__(256) void quant_tensor_kernel(const uint16_t* __restrict__ x, long n,
+                                                           const float* __restrict__ inv_scale,
+                                                           uint8_t* __restrict__ q) {
+  const float inv = *inv_scale;
+  for (long i = ((long)blockIdx.x * 256 + threadIdx.x) * 8; i < n; i += (long)gridDim.x * 256 * 8) {
+    float f[8];
+    load8<DT>(x + i, f);
+    uint32_t c[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c[e] = e4m3_encode(f[e] * inv);
+    *(uint2*)(q + i) = pack8(c);
+  }
+}
+
+bool act_dtype_ok(int dt) { return dt == TI_DTYPE_F16 || dt == TI_DTYPE_BF16; }
+
+}  // namespace
+}  // namespace fp8
+}  // namespace ti
+
+using namespace ti;
+using namespace ti::fp8;
+
+extern "C" int ti_fp8_quant_per_token(const void* x, int x_dtype, int M, int K, float eps,
+                                      uint8_t* xq, float* xs, hipStream_t stream) {
+  TI_CHECK_ARG(x && xq && xs, "ti_fp8_quant_per_token: null pointer");
+  TI_CHECK_ARG(act_dtype_ok(x_dtype), "ti_fp8_quant_per_token: x must be fp16 or bf16");
+  TI_CHECK_SHAPE(M >= 0 && K > 0 && K % 8 == 0, "ti_fp8_quant_per_token: need K %% 8 == 0 (K=%d)", K);
+  TI_CHECK_ARG(((uintptr_t)x & 15) == 0 && ((uintptr_t)xq & 7) == 0,
+               "ti_fp8_quant_per_token: x must be 16-byte and xq 8-byte aligned");
+  if (M == 0) return TI_OK;
+  if (x_dtype == TI_DTYPE_F16)
+    hipLaunchKernelGGL(quant_per_token_kernel<TI_DTYPE_F16>, dim3(M), dim3(256), 0, stream,
+                       (const uint16_t*)x, K, xq, xs, eps);
+  else
+    hipLaunchKernelGGL(quant_per_token_kernel<TI_DTYPE_BF16>, dim3(M), dim3(256), 0, stream,
+                       (const uint16_t*)x, K, xq, xs, eps);
+  TI_CHECK_LAUNCH("ti_fp8_quant_per_token");
+  return TI_OK;
+}
+
+extern "C" int ti_fp8_quant_block(const void* x, int x_dtype, int M, int K, int block_size,
+                                  int round_scale, uint8_t* xq, float* xs, hipStream_t stream) {
+  TI_CHECK_ARG(x && xq && xs, "ti_fp8_quant_block: null pointer");
+  TI_CHECK_ARG(act_dtype_ok(x_dtype), "ti_fp8_quant_block: x must be fp16 or bf16");
+  TI_CHECK_SHAPE(block_size == 128, "ti_fp8_quant_block: block_size must be 128 (got %d)", block_size);
+  TI_CHECK_SHAPE(M >= 0 && K > 0 && K % 128 == 0, "ti_fp8_quant_block: need K %% 128 == 0 (K=%d)", K);
+  TI_CHECK_ARG(((uintptr_t)x & 3) == 0 && ((uintptr_t)xq & 1) == 0,
+               "ti_fp8_quant_block: x must be 4-byte and xq 2-byte aligned");
+  if (M == 0) return TI_OK;
+  const long blocks = (long)M * (K / 128);
+  dim3 grid((unsigned)((blocks + 3) / 4));
+#define TI_QB(DT, P2)                                                                             \
+  hipLaunchKernelGGL((quant_block_kernel<DT, P2>), grid, dim3(256), 0, stream, (const uint16_t*)x, \
+                     M, K, xq, xs)
+  if (x_dtype == TI_DTYPE_F16) {
+    if (round_scale) TI_QB(TI_DTYPE_F16, true); else TI_QB(TI_DTYPE_F16, false);
+  } else {
+    if (round_scale) TI_QB(TI_DTYPE_BF16, true); else TI_QB(TI_DTYPE_BF16, false);
+  }
+#undef TI_QB
+  TI_CHECK_LAUNCH("ti_fp8_quant_block");
+  return TI_OK;
+}
+
+extern "C" int ti_fp8_quant_tensor(const void* x, int x_dtype, long n, const float* inv_scale,
+                                   uint8_t* xq, hipStream_t stream) {
+  TI_CHECK_ARG(x && xq && inv_scale, "ti_fp8_quant_tensor: null pointer");
+  TI_CHECK_ARG(act_dtype_ok(x_dtype), "ti_fp8_quant_tensor: x must be fp16 or bf16");
+  TI_CHECK_SHAPE(n >= 0 && n % 8 == 0, "ti_fp8_quant_tensor: need n %% 8 == 0 (n=%ld)", n);
+  TI_CHECK_ARG(((uintptr_t)x & 15) == 0 && ((uintptr_t)xq & 7) == 0,
+               "ti_fp8_quant_tensor: x must be 16-byte and xq 8-byte aligned");
+  if (n == 0) return TI_OK;
+  long blocks = (n / 8 + 255) / 256;
+  dim3 grid((unsigned)(blocks < 4096 ? blocks : 4096));
+  if (x_dtype == TI_DTYPE_F16)
+    hipLaunchKernelGGL(quant_tensor_kernel<TI_DTYPE_F16>, grid, dim3(256), 0, stream,
+                       (const uint16_t*)x, n, inv_scale, xq);
+  else
+    hipLaunchKernelGGL(quant_tensor_kernel<TI_DTYPE_BF16>, grid, dim3(256), 0, stream,
+                       (const uint16_t*)x, n, inv_scale, xq);
+  TI_CHECK_LAUNCH("ti_fp8_quant_tensor");
+  return TI_OK;
+}

@@ -26,6 +26,7 @@
 // by the last-arriving workgroup of a column block in split order (agent-scope
 // stores and loads of fp32 partials + a ticket), so results are deterministic.
 #include "int4_decode.h"
+#include "lds_dma.h"
 
 namespace ti {
 namespace int4 {
@@ -33,31 +34,6 @@ namespace int4 {
 namespace {
 
 constexpr int kWaves = 4;
-
-__device__ __forceinline__ uint32_t lds_offset(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
-}
-
-// 16 bytes per lane, global -> LDS at lds_base + 16 * lane.
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base))
-               : "memory");
-}
-
-// 4 bytes per lane, global -> LDS at lds_base + 4 * lane.
-__device__ __forceinline__ void dma4(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-               :
-               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base))
-               : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vm_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(N) : "memory");
-}
 
 template <int DT, int MR, int NT, int WK, int R, int SPLIT>
 __global__ __launch_bounds__(64 * kWaves) void w4a16_decode_kernel(
@@ -192,7 +168,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_decode_kernel(
     compute_group<DT, MT, NT>(w, a, sc, acc);
   }
   // No DMA may still be writing LDS when it is reused or the workgroup ends.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  wait_vm_all();
 
   // ---- add the WK partial sums through LDS (fixed wk order) ----
   float* red = (float*)smem;

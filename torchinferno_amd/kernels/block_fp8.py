@@ -1,0 +1,95 @@
+"""DeepSeek-style 128x128 block-scaled FP8 on MI355X -- drop-in for the reference's
+``act_quant`` / ``fp8_gemm`` (src/torchinferno/kernels/deepseek_v4_tilelang.py:147-173,
+207-223; kernels deepseek_v4_tilelang_definitions.py:273-331,436-485).
+
+``act_quant(x)``: 1x128 activation quant, ``s = max(amax, 1e-4) / 448`` (or the
+power-of-two ceiling when ``scale_fmt`` is set), ``y = clamp(x / s, +-448)``.
+``fp8_gemm(a, a_s, b, b_s)``: ``C = sum_kb (a . b^T)_kb * a_s[:, kb] * b_s[n/128, kb]``,
+bf16 out.  Both run libti_quant.so's gfx950 kernels.  Scales are fp32; the
+reference's ``float8_e8m0fnu`` scale storage is not supported (ValueError).
+"""
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from .. import _lib
+from .fp8 import FP8_E4M3, _ws_args
+
+BLOCK = 128
+
+
+def _check_scale_dtype(scale_dtype: torch.dtype) -> None:
+    if scale_dtype != torch.float32:
+        raise ValueError("only fp32 block scales are supported (float8_e8m0fnu storage is not)")
+
+
+def act_quant(
+    x: Tensor,
+    block_size: int = BLOCK,
+    scale_fmt: str | None = None,
+    scale_dtype: torch.dtype = torch.float32,
+    inplace: bool = False,
+) -> Tensor | tuple[Tensor, Tensor]:
+    """Block-wise FP8 activation quant.  Returns ``(y e4m3 [..., N], s fp32 [..., N/128])``;
+    with ``inplace=True`` writes the quantize-dequantize round trip back into ``x``
+    (bf16/fp16) and returns it, as the reference does."""
+    n = x.size(-1)
+    if block_size != BLOCK:
+        raise ValueError("FP8 block quantization supports block_size=128 only")
+    if n % block_size:
+        raise ValueError("FP8 quantization width must be divisible by block size")
+    _check_scale_dtype(scale_dtype)
+    _lib.require_device(x)
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("FP8 block quantization input must be bf16 or fp16")
+    value = x.contiguous()
+    rows = value.numel() // n
+    y = torch.empty(value.shape, dtype=FP8_E4M3, device=x.device)
+    s = torch.empty((*value.shape[:-1], n // block_size), dtype=torch.float32, device=x.device)
+    _lib.call("ti_fp8_quant_block", value.data_ptr(), _lib.dtype_code(value.dtype), rows, n, block_size,
+              int(scale_fmt is not None), y.data_ptr(), s.data_ptr(), _lib.stream_of(value))
+    if inplace:
+        deq = y.view(rows, n // block_size, block_size).float() * s.view(rows, -1, 1)
+        x.copy_(deq.view(x.shape).to(x.dtype))
+        return x
+    return y, s
+
+
+def fp8_gemm(
+    a: Tensor,
+    a_s: Tensor,
+    b: Tensor,
+    b_s: Tensor,
+    scale_dtype: torch.dtype = torch.float32,
+) -> Tensor:
+    """``C[M,N] = A[M,K] @ B[N,K]^T`` with per-128 block FP8 scaling on both A and B
+    (bf16 out).  ``a`` e4m3 ``[..., K]``, ``a_s`` fp32 ``[..., K/128]``, ``b`` e4m3 ``[N, K]``,
+    ``b_s`` fp32 ``[ceil(N/128), K/128]``."""
+    if not all(t.is_contiguous() for t in (a, a_s, b, b_s)):
+        raise ValueError("FP8 GEMM inputs and scales must be contiguous")
+    _check_scale_dtype(scale_dtype)
+    if a.dtype != FP8_E4M3 or b.dtype != FP8_E4M3:
+        raise ValueError("FP8 GEMM operands must be float8_e4m3fn")
+    if a_s.dtype != torch.float32 or b_s.dtype != torch.float32:
+        raise ValueError("FP8 GEMM scales must be fp32")
+    _lib.require_device(a, a_s, b, b_s)
+    k = a.size(-1)
+    m = a.numel() // k
+    n = b.size(0)
+    if b.ndim != 2 or b.size(1) != k:
+        raise ValueError("FP8 GEMM weight must be [N, K] with the activation's K")
+    if a_s.numel() != m * (k // BLOCK) or tuple(b_s.shape) != (-(-n // BLOCK), -(-k // BLOCK)):
+        raise ValueError("FP8 GEMM block scales must be a_s [M, K/128] and b_s [ceil(N/128), K/128]")
+    out = torch.empty((*a.shape[:-1], n), dtype=torch.bfloat16, device=a.device)
+    ws, ws_bytes = _ws_args(a.device, m, n, k, 1)
+    _lib.call("ti_fp8_gemm_block", a.data_ptr(), a_s.data_ptr(), b.data_ptr(), b_s.data_ptr(), out.data_ptr(),
+              _lib.TI_DTYPE_BF16, m, n, k, ws, ws_bytes, _lib.stream_of(a))
+    return out
+
+
+def linear(x: Tensor, weight: Tensor, weight_scale: Tensor) -> Tensor:
+    """DeepSeek ``linear`` for an e4m3 weight (src/torchinferno/models/deepseek_v4/
+    tensor_parallel.py:195-207): ``act_quant`` then ``fp8_gemm``, bf16 out."""
+    xq, xs = act_quant(x)
+    return fp8_gemm(xq, xs, weight, weight_scale)
