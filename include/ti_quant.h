@@ -146,6 +146,40 @@ int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, const uint8_t* b,
                       const float* b_scale, void* out, int out_dtype, int M, int N, int K,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Routed FP8 block-scaled MoE (DeepSeek expert shapes).
+ * ------------------------------------------------------------------------- */
+
+/* Router: per token, softmax over E fp32 logits, top-k experts (descending,
+ * ties to the lower index), their softmax scores, renormalised to sum 1
+ * (w / max(sum, 1e-20)) when renormalize != 0, times route_scale.  Replaces
+ * DSv4 Gate.forward (src/torchinferno/models/deepseek_v4/tensor_parallel.py:
+ * 760-780) / DeepSeekMoEGate.forward (src/torchinferno/models/deepseek_v32/
+ * model.py:692-722) for softmax scoring without group limits.
+ * logits [T,E] (E <= 1024), k <= 16; weights fp32 [T,k], ids int32 [T,k]. */
+int ti_moe_route_topk(const float* logits, int T, int E, int k, int renormalize,
+                      float route_scale, float* topk_weights, int32_t* topk_ids,
+                      hipStream_t stream);
+
+/* Workspace bytes of ti_fp8_moe (all intermediates; no allocation inside). */
+size_t ti_fp8_moe_workspace_bytes(int T, int k, int E, int H, int I);
+
+/* out[t] = bf16( sum over t's routed experts e, in expert order, of
+ *   w2_e( bf16( w[t,e] * silu(w1_e x) * (w3_e x) ) ) )
+ * with every w*_e a 128x128 block-scaled e4m3 Linear (1x128 activation quant,
+ * bf16 output).  Replaces fused_mxfp4_moe and its align/grouped GEMMs
+ * (src/torchinferno/kernels/deepseek_v4_marlin.py:267-411) and computes the
+ * per-expert loop of MoE.forward (tensor_parallel.py:882-914).
+ *   hidden bf16 [T,H]; topk_weights fp32 [T,k]; topk_ids int32 [T,k] (ids
+ *   outside [0,E) are skipped); w13 e4m3 [E, 2I, H] = [w1; w3] per expert,
+ *   s13 fp32 [E, 2I/128, H/128]; w2 e4m3 [E, H, I], s2 fp32 [E, H/128, I/128];
+ *   clamp_limit > 0 clamps gate <= limit and |up| <= limit (swiglu_limit);
+ *   out bf16 [T,H].  H, I multiples of 128.  Deterministic. */
+int ti_fp8_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids,
+               int T, int k, const uint8_t* w13, const float* s13, const uint8_t* w2,
+               const float* s2, int E, int H, int I, float clamp_limit, void* out,
+               void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

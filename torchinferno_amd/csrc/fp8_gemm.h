@@ -6,7 +6,7 @@
 namespace ti {
 namespace fp8 {
 
-constexpr int kNumKinds = 7;
+constexpr int kNumKinds = 10;
 
 struct GemmArgs {
   const uint8_t* a;   // [M, K] e4m3
@@ -19,18 +19,35 @@ struct GemmArgs {
   int* tickets;       // one per tile, zero between calls
   int M, N, K;
   int splits, tiles_m, tiles_n;
+  int group_m;        // tile rows per raster group
+  // Gather / grouped (MoE) mode:
+  const int* row_index;     // A (and block-mode sa) row of output row p; nullptr = p
+  int grouped;              // 1: m-tiles come from the device tables below
+  const int* tile_expert;   // [max m-tiles] expert of each m-tile
+  const int* tile_row0;     // first output row of each m-tile
+  const int* tile_rows;     // rows of each m-tile (<= BM)
+  const int* num_mtiles;    // device scalar: m-tiles in use
+  long b_expert_stride;     // bytes between experts' [N, K] weights
+  long sb_expert_stride;    // floats between experts' weight-scale grids
 };
 
 struct GemmPlan {
   int kind;     // tile configuration (fp8_gemm.hip)
   int tiles_m, tiles_n;
   int splits;
+  int group_m;
 };
 
 GemmPlan make_gemm_plan(int M, int N, int K, int smode);
 size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N);
 size_t gemm_ticket_bytes(const GemmPlan& p);
 void launch_gemm(const GemmPlan& p, int smode, int odt, const GemmArgs& x, hipStream_t stream);
+
+// Grouped block-scaled GEMM (bf16 out) over a device m-tile table; kind is one
+// of 2 (128x128), 5 (64x128), 6 (16x128), 9 (256x128).
+int grouped_bm(int kind);
+int grouped_bn(int kind);
+void launch_gemm_grouped(int kind, const GemmArgs& x, int max_mtiles, hipStream_t stream);
 
 }  // namespace fp8
 }  // namespace ti

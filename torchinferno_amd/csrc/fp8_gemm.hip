@@ -66,8 +66,15 @@ struct Mfma<16> {
   static __device__ __forceinline__ int chunk(int, int lane) { return (lane >> 4) * 2; }
 };
 
-// Byte offset of 16-byte chunk c of row r in a swizzled [rows x 128 B] slab.
-__device__ __forceinline__ int swz(int r, int c) { return (r * 8 + (c ^ ((r >> 1) & 7))) * 16; }
+// Byte offset of 16-byte chunk c of row r in a swizzled [rows x BK bytes] slab:
+// CPR = BK/16 chunks per row, RP = 256/BK rows per 256-byte bank period; chunk c
+// sits at position c ^ ((r / RP) % CPR), so 16 consecutive rows reading one
+// chunk cover all 64 banks.
+template <int BK>
+__device__ __forceinline__ int swz(int r, int c) {
+  constexpr int CPR = BK / 16, RP = 256 / BK;
+  return (r * CPR + (c ^ ((r / RP) % CPR))) * 16;
+}
 
 template <int ODT>
 __device__ __forceinline__ uint16_t out_bits(float v) {
@@ -75,7 +82,7 @@ __device__ __forceinline__ uint16_t out_bits(float v) {
   else return f32_to_bf16_bits(v);
 }
 
-template <int BM, int BN, int WGM, int WGN, int MF, int R, int SMODE, int SPLIT, int ODT>
+template <int BM, int BN, int BK, int WGM, int WGN, int MF, int R, int SMODE, int SPLIT, int ODT>
 __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
   using MM = Mfma<MF>;
   typedef typename MM::acc_t acc_t;
@@ -84,7 +91,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
   constexpr int FM = TM / MF, FN = TN / MF;
   static_assert(FM >= 1 && FN >= 1 && TM % MF == 0 && TN % MF == 0, "wave tile must hold whole MFMA tiles");
   static_assert(SMODE == 0 || 128 % TN == 0, "block scales need a wave's columns inside one 128 block");
-  constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
+  static_assert(BK == 128 || (BK == 64 && MF == 32), "16x16x128 MFMAs need 128-byte K steps");
+  constexpr int KS = BK / (MF == 32 ? 64 : 128);  // MFMAs per K step
+  constexpr int CPR = BK / 16;                     // 16-byte chunks per row
+  constexpr int RPI = 1024 / BK;                   // rows per 1 KiB DMA
+  constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
   // Block mode also stages the step's BM activation scales and (one 256-byte
   // DMA) the weight scales of the tile's 128-column blocks.
   constexpr int SA_BYTES = SMODE == 1 ? ((BM * 4 + 255) / 256) * 256 + 256 : 0;
@@ -104,20 +115,40 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
   const int wave = threadIdx.x >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
   const int M = x.M, N = x.N, K = x.K;
-  const int KT = K / 128;
+  const int KT = K / BK;      // K steps
+  const int KB = K / 128;     // 128-wide scale blocks
 
-  // ---- tile of this workgroup (XCD-contiguous runs of a grouped raster) ----
-  int t = blockIdx.x;
-  const int nt = gridDim.x;
-  if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);
-  const int tiles_m = x.tiles_m, tiles_n = x.tiles_n;
-  constexpr int GM = 8;
-  const int group = t / (GM * tiles_n);
-  const int first_m = group * GM;
-  const int gsz = min(tiles_m - first_m, GM);
-  const int tin = t - group * GM * tiles_n;
-  const int tm = first_m + tin % gsz, tn = tin / gsz;
-  const int m0 = tm * BM, n0 = tn * BN;
+  // ---- tile of this workgroup ----
+  int m0, n0, Mlim;
+  const uint8_t* bmat = x.b;
+  const float* sbmat = x.sb;
+  const int tiles_n = x.tiles_n;
+  if (x.grouped) {
+    // Grouped (MoE) launch: blockIdx.x = m-tile * tiles_n + n-tile over a device
+    // table of (expert, first row, rows) m-tiles; surplus workgroups exit.
+    const int mt = blockIdx.x / tiles_n;
+    if (mt >= *x.num_mtiles) return;
+    const int e = x.tile_expert[mt];
+    m0 = x.tile_row0[mt];
+    Mlim = m0 + x.tile_rows[mt];
+    n0 = (blockIdx.x % tiles_n) * BN;
+    bmat += (long)e * x.b_expert_stride;
+    sbmat += (long)e * x.sb_expert_stride;
+  } else {
+    // XCD-contiguous runs of a grouped raster.
+    int t = blockIdx.x;
+    const int nt = gridDim.x;
+    if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);
+    const int tiles_m = x.tiles_m;
+    const int GM = x.group_m;
+    const int group = t / (GM * tiles_n);
+    const int first_m = group * GM;
+    const int gsz = min(tiles_m - first_m, GM);
+    const int tin = t - group * GM * tiles_n;
+    m0 = (first_m + tin % gsz) * BM;
+    n0 = (tin / gsz) * BN;
+    Mlim = M;
+  }
 
   const int split = blockIdx.y;
   const int per = cdiv(KT, x.splits);
@@ -127,30 +158,53 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
   const uint32_t ring0 = lds_offset(smem);
   const int n_mine = (NI - wave + W - 1) / W;  // DMAs of this wave per stage
 
+  // Source row pointer, per-step stride multiplier and LDS offset of each of
+  // this wave's DMAs, fixed for the whole K walk (gather indices are read here,
+  // once, so no ordinary load sits between the ring's DMAs).
+  const uint8_t* dsrc[NI_HI];
+  uint32_t dlds[NI_HI];
+  bool dwide[NI_HI];
+#pragma unroll
+  for (int u = 0; u < NI_HI; ++u) {
+    const int id = min(wave + u * W, NI - 1);
+    if (id < NI_AB) {
+      const bool is_a = id < A_BYTES / 1024;
+      const int j = is_a ? id : id - A_BYTES / 1024;
+      const int r = RPI * j + lane / CPR;
+      const int c = (lane % CPR) ^ ((r / (256 / BK)) % CPR);
+      long row;
+      if (is_a) {
+        row = min(m0 + r, Mlim - 1);
+        if (x.row_index) row = x.row_index[row];
+      } else {
+        row = min(n0 + r, N - 1);
+      }
+      dsrc[u] = (is_a ? x.a : bmat) + row * K + c * 16;
+      dlds[u] = (uint32_t)((is_a ? 0 : A_BYTES) + j * 1024);
+      dwide[u] = true;
+    } else if (id < NI_AB + NI_SA) {
+      const int j = id - NI_AB;
+      long row = min(m0 + min(j * 64 + lane, BM - 1), Mlim - 1);
+      if (x.row_index) row = x.row_index[row];
+      dsrc[u] = (const uint8_t*)(x.sa + row * KB);
+      dlds[u] = (uint32_t)(A_BYTES + B_BYTES + j * 256);
+      dwide[u] = false;
+    } else {
+      const int nb = min(n0 / 128 + lane, (N + 127) / 128 - 1);
+      dsrc[u] = (const uint8_t*)(sbmat + (long)nb * KB);
+      dlds[u] = (uint32_t)(A_BYTES + B_BYTES + NI_SA * 256);
+      dwide[u] = false;
+    }
+  }
+
   auto issue = [&](int i) {
     const uint32_t base = ring0 + (uint32_t)((i % R) * STAGE);
     const long kk = ks0 + i;
 #pragma unroll
     for (int u = 0; u < NI_HI; ++u) {
-      const int id = wave + u * W;
-      if (id >= NI) break;
-      if (id < NI_AB) {
-        const bool is_a = id < A_BYTES / 1024;
-        const int j = is_a ? id : id - A_BYTES / 1024;
-        const int r = 8 * j + (lane >> 3);
-        const int c = (lane & 7) ^ ((r >> 1) & 7);
-        const uint8_t* src = is_a ? x.a + (long)min(m0 + r, M - 1) * K
-                                  : x.b + (long)min(n0 + r, N - 1) * K;
-        dma16(src + kk * 128 + c * 16, base + (uint32_t)((is_a ? 0 : A_BYTES) + j * 1024));
-      } else if (id < NI_AB + NI_SA) {
-        const int j = id - NI_AB;
-        const int e = j * 64 + lane;
-        const int row = min(m0 + min(e, BM - 1), M - 1);
-        dma4(x.sa + (long)row * KT + kk, base + (uint32_t)(A_BYTES + B_BYTES + j * 256));
-      } else {
-        const int nb = min(n0 / 128 + lane, (N + 127) / 128 - 1);
-        dma4(x.sb + (long)nb * KT + kk, base + (uint32_t)(A_BYTES + B_BYTES + NI_SA * 256));
-      }
+      if (wave + u * W >= NI) break;
+      if (dwide[u]) dma16(dsrc[u] + kk * BK, base + dlds[u]);
+      else dma4((const float*)dsrc[u] + kk * BK / 128, base + dlds[u]);
     }
   };
 
@@ -187,21 +241,21 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
     const uint8_t* sB = st + A_BYTES;
     if constexpr (SMODE == 0) {
 #pragma unroll
-      for (int ks = 0; ks < MM::KS; ++ks) {
+      for (int ks = 0; ks < KS; ++ks) {
         const int c0 = MM::chunk(ks, lane);
         i32x8 af[FM], bf[FN];
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm) {
           const int r = arow0 + fm * MF;
-          const i32x4 lo = *(const i32x4*)(sA + swz(r, c0));
-          const i32x4 hi = *(const i32x4*)(sA + swz(r, c0 + 1));
+          const i32x4 lo = *(const i32x4*)(sA + swz<BK>(r, c0));
+          const i32x4 hi = *(const i32x4*)(sA + swz<BK>(r, c0 + 1));
           af[fm] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
           const int r = brow0 + fn * MF;
-          const i32x4 lo = *(const i32x4*)(sB + swz(r, c0));
-          const i32x4 hi = *(const i32x4*)(sB + swz(r, c0 + 1));
+          const i32x4 lo = *(const i32x4*)(sB + swz<BK>(r, c0));
+          const i32x4 hi = *(const i32x4*)(sB + swz<BK>(r, c0 + 1));
           bf[fn] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
 #pragma unroll
@@ -214,27 +268,27 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
       const float sbv = sS[NI_SA * 64 + (wn * TN) / 128];
       // All B fragments of the step stay in registers; A is read one M tile
       // at a time (bounds register use with the per-tile partial sums).
-      i32x8 bf[MM::KS][FN];
+      i32x8 bf[KS][FN];
 #pragma unroll
-      for (int ks = 0; ks < MM::KS; ++ks) {
+      for (int ks = 0; ks < KS; ++ks) {
         const int c0 = MM::chunk(ks, lane);
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
           const int r = brow0 + fn * MF;
-          const i32x4 lo = *(const i32x4*)(sB + swz(r, c0));
-          const i32x4 hi = *(const i32x4*)(sB + swz(r, c0 + 1));
+          const i32x4 lo = *(const i32x4*)(sB + swz<BK>(r, c0));
+          const i32x4 hi = *(const i32x4*)(sB + swz<BK>(r, c0 + 1));
           bf[ks][fn] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
       }
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
-        i32x8 af[MM::KS];
+        i32x8 af[KS];
         const int r = arow0 + fm * MF;
 #pragma unroll
-        for (int ks = 0; ks < MM::KS; ++ks) {
+        for (int ks = 0; ks < KS; ++ks) {
           const int c0 = MM::chunk(ks, lane);
-          const i32x4 lo = *(const i32x4*)(sA + swz(r, c0));
-          const i32x4 hi = *(const i32x4*)(sA + swz(r, c0 + 1));
+          const i32x4 lo = *(const i32x4*)(sA + swz<BK>(r, c0));
+          const i32x4 hi = *(const i32x4*)(sA + swz<BK>(r, c0 + 1));
           af[ks] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
         float srow[MM::NACC];
@@ -246,7 +300,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 #pragma unroll
           for (int e = 0; e < MM::NACC; ++e) p[e] = 0.f;
 #pragma unroll
-          for (int ks = 0; ks < MM::KS; ++ks) p = MM::mma(af[ks], bf[ks][fn], p);
+          for (int ks = 0; ks < KS; ++ks) p = MM::mma(af[ks], bf[ks][fn], p);
 #pragma unroll
           for (int e = 0; e < MM::NACC; ++e) acc[fm][fn][e] = __builtin_fmaf(p[e], srow[e], acc[fm][fn][e]);
         }
@@ -268,7 +322,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 #pragma unroll
         for (int e = 0; e < MM::NACC; ++e) {
           const int row = m0 + wm * TM + fm * MF + MM::row(e, lane);
-          if (row < M && col < N) {
+          if (row < Mlim && col < N) {
             float v = acc[fm][fn][e];
             if constexpr (SMODE == 0) v = v * x.sa[(long)row * x.sa_stride] * sbn;
             x.out[(long)row * N + col] = out_bits<ODT>(v);
@@ -313,46 +367,61 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 }
 
 // ---------------------------------------------------------------------------
-// Tile configurations (kind):
-//   0  BM=256 BN=256, 8 waves 2x4 (wave 128x64), 32x32 MFMA, 2 stages  -- prefill
-//   1  BM=256 BN=256, 4 waves 2x2 (wave 128x128), 32x32 MFMA, 2 stages -- prefill
-//   2  BM=128 BN=128, 4 waves 2x2 (wave 64x64),  32x32 MFMA, 3 stages -- mid M
-//   3  BM=16  BN=256, 4 waves 1x4 (wave 16x64),  16x16 MFMA, 4 stages -- decode
-//   4  BM=32  BN=256, 4 waves 1x4 (wave 32x64),  16x16 MFMA, 4 stages -- decode
-//   5  BM=64  BN=128, 4 waves 1x4 (wave 64x32),  16x16 MFMA, 4 stages -- small M
-//   6  BM=16  BN=128, 4 waves 1x4 (wave 16x32),  16x16 MFMA, 6 stages -- decode
-template <int BM, int BN, int WGM, int WGN, int MF, int R, int SMODE>
+// Tile configurations (kind):                                        K step  stages
+//   0  BM=256 BN=256, 8 waves 2x4 (wave 128x64),  32x32 MFMA            64      4   -- prefill
+//   1  BM=256 BN=256, 8 waves 2x4 (wave 128x64),  32x32 MFMA            128     2   -- prefill
+//   2  BM=128 BN=128, 4 waves 2x2 (wave 64x64),   32x32 MFMA            128     3   -- mid M
+//   3  BM=16  BN=256, 4 waves 1x4 (wave 16x64),   16x16 MFMA            128     4   -- decode
+//   4  BM=32  BN=256, 4 waves 1x4 (wave 32x64),   16x16 MFMA            128     4   -- decode
+//   5  BM=64  BN=128, 4 waves 1x4 (wave 64x32),   16x16 MFMA            128     4   -- small M
+//   6  BM=16  BN=128, 4 waves 1x4 (wave 16x32),   16x16 MFMA            128     6   -- decode
+//   7  BM=128 BN=128, 4 waves 2x2 (wave 64x64),   32x32 MFMA            64      6   -- mid M
+//   8  BM=256 BN=128, 4 waves 2x2 (wave 128x64),  32x32 MFMA            64      6   -- prefill
+//   9  BM=256 BN=128, 8 waves 4x2 (wave 64x64),   32x32 MFMA            128     3   -- prefill
+template <int BM, int BN, int BK, int R, int SMODE>
 constexpr int cfg_lds() {
-  return R * (BM * 128 + BN * 128 + (SMODE == 1 ? ((BM * 4 + 255) / 256) * 256 + 256 : 0));
+  return R * (BM * BK + BN * BK + (SMODE == 1 ? ((BM * 4 + 255) / 256) * 256 + 256 : 0));
 }
 
-template <int BM, int BN, int WGM, int WGN, int MF, int R, int SMODE, int ODT>
+template <int BM, int BN, int BK, int WGM, int WGN, int MF, int R, int SMODE, int ODT>
 void launch_cfg(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
-  constexpr int lds = cfg_lds<BM, BN, WGM, WGN, MF, R, SMODE>();
+  constexpr int lds = cfg_lds<BM, BN, BK, R, SMODE>();
+  static_assert(lds <= 160 * 1024, "tile configuration exceeds the 160 KiB LDS");
   dim3 grid(p.tiles_m * p.tiles_n, p.splits);
   if (p.splits > 1)
-    hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, WGM, WGN, MF, R, SMODE, 2, ODT>), grid, dim3(64 * WGM * WGN),
+    hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, BK, WGM, WGN, MF, R, SMODE, 2, ODT>), grid, dim3(64 * WGM * WGN),
                        lds, stream, x);
   else
-    hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, WGM, WGN, MF, R, SMODE, 0, ODT>), grid, dim3(64 * WGM * WGN),
+    hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, BK, WGM, WGN, MF, R, SMODE, 0, ODT>), grid, dim3(64 * WGM * WGN),
                        lds, stream, x);
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, int MF, int R>
+void launch_grouped_cfg(const GemmArgs& x, int max_mtiles, hipStream_t stream) {
+  constexpr int lds = cfg_lds<BM, BN, BK, R, 1>();
+  dim3 grid((unsigned)(max_mtiles * x.tiles_n), 1);
+  hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, BK, WGM, WGN, MF, R, 1, 0, TI_DTYPE_BF16>), grid,
+                     dim3(64 * WGM * WGN), lds, stream, x);
 }
 
 template <int SMODE, int ODT>
 void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
   switch (p.kind) {
-    case 0: launch_cfg<256, 256, 2, 4, 32, 2, SMODE, ODT>(p, x, stream); break;
-    case 1: launch_cfg<256, 256, 2, 2, 32, 2, SMODE, ODT>(p, x, stream); break;
-    case 2: launch_cfg<128, 128, 2, 2, 32, 3, SMODE, ODT>(p, x, stream); break;
-    case 3: launch_cfg<16, 256, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
-    case 4: launch_cfg<32, 256, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
-    case 5: launch_cfg<64, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
-    default: launch_cfg<16, 128, 1, 4, 16, 6, SMODE, ODT>(p, x, stream); break;
+    case 0: launch_cfg<256, 256, 64, 2, 4, 32, 4, SMODE, ODT>(p, x, stream); break;
+    case 1: launch_cfg<256, 256, 128, 2, 4, 32, 2, SMODE, ODT>(p, x, stream); break;
+    case 2: launch_cfg<128, 128, 128, 2, 2, 32, 3, SMODE, ODT>(p, x, stream); break;
+    case 3: launch_cfg<16, 256, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
+    case 4: launch_cfg<32, 256, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
+    case 5: launch_cfg<64, 128, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
+    case 6: launch_cfg<16, 128, 128, 1, 4, 16, 6, SMODE, ODT>(p, x, stream); break;
+    case 7: launch_cfg<128, 128, 64, 2, 2, 32, 6, SMODE, ODT>(p, x, stream); break;
+    case 8: launch_cfg<256, 128, 64, 2, 2, 32, 6, SMODE, ODT>(p, x, stream); break;
+    default: launch_cfg<256, 128, 128, 4, 2, 32, 3, SMODE, ODT>(p, x, stream); break;
   }
 }
 
-const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16};
-const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128};
+const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256};
+const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128, 128, 128, 128};
 
 int env_int(const char* name, int dflt) {
   const char* e = getenv(name);
@@ -364,31 +433,50 @@ int env_int(const char* name, int dflt) {
 GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   GemmPlan p;
   const int KT = K / 128;
-  // Heuristic (MI355X, 256 CUs): skinny M streams B with a 16/32-row tile and
-  // split-K up to ~2 workgroups per CU; large M uses 256x256 tiles, 128x128
-  // when 256x256 leaves the chip under-filled.
-  if (M <= 16) p.kind = N >= 16384 ? 6 : 3;
-  else if (M <= 32) p.kind = 4;
-  else if (M <= 128) p.kind = 5;
-  else {
-    const long big = (long)cdiv(M, 256) * cdiv(N, 256);
-    p.kind = big >= 192 ? 0 : 2;
+  // Measured on MI355X at the Llama-3-70B / DeepSeek-V3 shapes (BASELINE
+  // configs 2 and 3): skinny M streams B with 16- or 64-row tiles, split over K
+  // when too few column tiles cover the 256 CUs; larger M takes the largest
+  // tile that still gives every CU a workgroup (256x256, then 256x128 -- block
+  // scales favour it from 128 tiles -- then 128x128, split over K below 128).
+  auto tiles = [&](int bm, int bn) { return (long)cdiv(M, bm) * cdiv(N, bn); };
+  int splits = 1;
+  if (M <= 64) {
+    p.kind = M <= 16 ? 6 : 5;
+    const long t = tiles(kBM[p.kind], kBN[p.kind]);
+    splits = t >= 72 ? 1 : (int)(cdiv(256, (int)t) < 4 ? cdiv(256, (int)t) : 4);
+  } else if (M <= 128) {
+    p.kind = 5;
+    splits = tiles(64, 128) >= 128 ? 1 : 2;
+  } else if (tiles(256, 256) >= 256) {
+    p.kind = 1;
+  } else if (tiles(256, 128) >= (smode == 1 ? 128 : 256)) {
+    p.kind = 9;
+  } else {
+    p.kind = 2;
+    splits = tiles(128, 128) > 128 ? 1 : 2;
   }
   p.kind = env_int("TI_ROCM_FP8_KIND", p.kind);
-  if (p.kind < 0 || p.kind >= kNumKinds) p.kind = 0;
+  if (p.kind < 0 || p.kind >= kNumKinds) p.kind = 1;
+  p.group_m = env_int("TI_ROCM_FP8_GROUP_M", 4);
+  if (p.group_m < 1) p.group_m = 1;
   p.tiles_m = cdiv(M, kBM[p.kind]);
   p.tiles_n = cdiv(N, kBN[p.kind]);
-  const long tiles = (long)p.tiles_m * p.tiles_n;
-  int splits = 1;
-  if (tiles < 256) {
-    splits = cdiv(512, (int)tiles);
-    const int cap = KT / 8 > 1 ? KT / 8 : 1;  // at least 8 K steps per split
-    splits = splits < cap ? splits : cap;
-  }
   splits = env_int("TI_ROCM_FP8_SPLITS", splits);
-  p.splits = splits < 1 ? 1 : (splits > KT ? KT : splits);
-  (void)smode;
+  splits = splits > KT / 4 ? KT / 4 : splits;  // at least 4 K blocks per split
+  p.splits = splits < 1 ? 1 : splits;
   return p;
+}
+
+int grouped_bm(int kind) { return kBM[kind]; }
+int grouped_bn(int kind) { return kBN[kind]; }
+
+void launch_gemm_grouped(int kind, const GemmArgs& x, int max_mtiles, hipStream_t stream) {
+  switch (kind) {
+    case 2: launch_grouped_cfg<128, 128, 128, 2, 2, 32, 3>(x, max_mtiles, stream); break;
+    case 5: launch_grouped_cfg<64, 128, 128, 1, 4, 16, 4>(x, max_mtiles, stream); break;
+    case 9: launch_grouped_cfg<256, 128, 128, 4, 2, 32, 3>(x, max_mtiles, stream); break;
+    default: launch_grouped_cfg<16, 128, 128, 1, 4, 16, 6>(x, max_mtiles, stream); break;
+  }
 }
 
 size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
@@ -438,7 +526,7 @@ static int gemm_common(const char* name, int smode, const uint8_t* a, const floa
   x.sa_stride = a_scale_stride; x.sb_stride = b_scale_stride;
   x.out = (uint16_t*)out;
   x.M = M; x.N = N; x.K = K;
-  x.splits = p.splits; x.tiles_m = p.tiles_m; x.tiles_n = p.tiles_n;
+  x.splits = p.splits; x.tiles_m = p.tiles_m; x.tiles_n = p.tiles_n; x.group_m = p.group_m;
   const size_t need = gemm_workspace_bytes(p, M, N);
   if (need) {
     if (!workspace || workspace_bytes < need) {

@@ -1,0 +1,139 @@
+"""Routed FP8 block-scaled MoE on MI355X -- drop-in for the reference's grouped expert
+path (src/torchinferno/kernels/deepseek_v4_marlin.py: ``prepare_mxfp4_experts``
+:194-264, ``fused_mxfp4_moe`` :311-411) with DeepSeek-V3-style FP8 experts
+(128x128 block scales) instead of MXFP4.
+
+``route_topk`` is the softmax gate (DSv4 ``Gate.forward``,
+src/torchinferno/models/deepseek_v4/tensor_parallel.py:760-780; V3.2
+``DeepSeekMoEGate.forward``, models/deepseek_v32/model.py:692-722 without group
+limits).  ``fused_fp8_moe`` computes, for every token, the sum over its routed
+experts of ``w2(w * silu(w1 x) * (w3 x))`` -- the per-expert loop of
+``MoE.forward`` (tensor_parallel.py:882-914) -- as one stream-ordered sequence of
+gfx950 kernels (``ti_fp8_moe``): no host synchronisation, deterministic output.
+"""
+from __future__ import annotations
+
+import threading
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor
+
+from .. import _lib
+from .fp8 import FP8_E4M3
+
+_ws_lock = threading.Lock()
+_workspaces: dict[int, Tensor] = {}
+
+
+@dataclass(frozen=True)
+class PreparedFp8Experts:
+    """One GPU's experts in the kernel layout: ``w13 = [w1; w3]`` per expert."""
+
+    w13: Tensor        # e4m3 [E, 2I, H]
+    w13_scale: Tensor  # fp32 [E, 2I/128, H/128]
+    w2: Tensor         # e4m3 [E, H, I]
+    w2_scale: Tensor   # fp32 [E, H/128, I/128]
+    expert_map: Tensor  # int32 [global experts] -> local index or -1
+    global_num_experts: int
+    hidden_size: int
+    intermediate_size: int
+
+
+def prepare_fp8_experts(w1: Tensor, w3: Tensor, w2: Tensor, w1_scale: Tensor, w3_scale: Tensor,
+                        w2_scale: Tensor, *, expert_start: int = 0,
+                        global_num_experts: int | None = None) -> PreparedFp8Experts:
+    """Stack one GPU's block-FP8 experts (the analogue of prepare_mxfp4_experts,
+    deepseek_v4_marlin.py:194-264).  ``w1``/``w3`` e4m3 ``[E, I, H]``, ``w2`` ``[E, H, I]``,
+    scales fp32 per 128x128 block.  Weight preparation: run once, before capture."""
+    if w1.ndim != 3 or w3.ndim != 3 or w2.ndim != 3:
+        raise ValueError("expert weights must be stacked [experts, output, K]")
+    if tuple(w1.shape) != tuple(w3.shape):
+        raise ValueError("w1 and w3 expert shapes must match")
+    e, inter, hidden = w1.shape
+    if tuple(w2.shape) != (e, hidden, inter):
+        raise ValueError("w2 expert shape does not match w1/w3")
+    if any(t.dtype != FP8_E4M3 for t in (w1, w3, w2)):
+        raise ValueError("expert weights must be float8_e4m3fn")
+    if hidden % 128 or inter % 128:
+        raise ValueError("hidden and intermediate sizes must be multiples of 128")
+    global_num_experts = e if global_num_experts is None else global_num_experts
+    expert_map = torch.full((global_num_experts,), -1, dtype=torch.int32, device=w1.device)
+    expert_map[expert_start:expert_start + e] = torch.arange(e, dtype=torch.int32, device=w1.device)
+    return PreparedFp8Experts(
+        w13=torch.cat((w1, w3), dim=1).contiguous(),
+        w13_scale=torch.cat((w1_scale, w3_scale), dim=1).float().contiguous(),
+        w2=w2.contiguous(),
+        w2_scale=w2_scale.float().contiguous(),
+        expert_map=expert_map,
+        global_num_experts=global_num_experts,
+        hidden_size=hidden,
+        intermediate_size=inter,
+    )
+
+
+def route_topk(logits: Tensor, k: int, *, renormalize: bool = True,
+               route_scale: float = 1.0) -> tuple[Tensor, Tensor]:
+    """Softmax top-k router: (weights fp32 [T,k], ids int32 [T,k]), descending."""
+    _lib.require_device(logits)
+    if logits.ndim != 2:
+        raise ValueError("router logits must be [tokens, experts]")
+    z = logits.float().contiguous()
+    t, e = z.shape
+    w = torch.empty((t, k), dtype=torch.float32, device=z.device)
+    ids = torch.empty((t, k), dtype=torch.int32, device=z.device)
+    _lib.call("ti_moe_route_topk", z.data_ptr(), t, e, k, int(renormalize), float(route_scale),
+              w.data_ptr(), ids.data_ptr(), _lib.stream_of(z))
+    return w, ids
+
+
+def _workspace(device: torch.device, nbytes: int) -> Tensor:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    with _ws_lock:
+        ws = _workspaces.get(idx)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+            _workspaces[idx] = ws
+        return ws
+
+
+def fused_fp8_moe(hidden_states: Tensor, topk_weights: Tensor, topk_ids: Tensor,
+                  experts: PreparedFp8Experts, *, clamp_limit: float = 0.0) -> Tensor:
+    """Grouped routed experts for one GPU (signature of fused_mxfp4_moe,
+    deepseek_v4_marlin.py:311-318).  ``topk_ids`` are global expert ids; routes to
+    experts this GPU does not hold contribute nothing.  Returns bf16 [T, H]."""
+    if hidden_states.ndim != 2 or not hidden_states.is_contiguous():
+        raise ValueError("hidden_states must be a contiguous matrix")
+    if hidden_states.dtype != torch.bfloat16:
+        raise ValueError("hidden_states must be bf16")
+    tokens, hidden = hidden_states.shape
+    if hidden != experts.hidden_size:
+        raise ValueError("hidden size does not match prepared experts")
+    if topk_ids.shape != topk_weights.shape or topk_ids.ndim != 2 or topk_ids.size(0) != tokens:
+        raise ValueError("topk ids/weights must be [tokens, k]")
+    _lib.require_device(hidden_states, topk_weights, topk_ids)
+    k = topk_ids.size(1)
+    local_ids = experts.expert_map[topk_ids.long()].to(torch.int32).contiguous()
+    weights = topk_weights.float().contiguous()
+    e_local = experts.w13.size(0)
+    inter = experts.intermediate_size
+    out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=hidden_states.device)
+    if tokens == 0:
+        return out
+    need = int(_lib.lib().ti_fp8_moe_workspace_bytes(tokens, k, e_local, hidden, inter))
+    ws = _workspace(hidden_states.device, need)
+    base = ws.data_ptr()
+    aligned = (base + 255) & ~255
+    _lib.call("ti_fp8_moe", hidden_states.data_ptr(), weights.data_ptr(), local_ids.data_ptr(), tokens, k,
+              experts.w13.data_ptr(), experts.w13_scale.data_ptr(), experts.w2.data_ptr(),
+              experts.w2_scale.data_ptr(), e_local, hidden, inter, float(clamp_limit), out.data_ptr(),
+              aligned, ws.numel() - (aligned - base), _lib.stream_of(hidden_states))
+    return out
+
+
+def moe_forward(hidden_states: Tensor, router_logits: Tensor, experts: PreparedFp8Experts, k: int, *,
+                renormalize: bool = True, route_scale: float = 1.0, clamp_limit: float = 0.0) -> Tensor:
+    """Router + routed experts: the routed part of DSv4 MoE.forward (without the
+    shared expert and the cross-GPU all-reduce)."""
+    w, ids = route_topk(router_logits, k, renormalize=renormalize, route_scale=route_scale)
+    return fused_fp8_moe(hidden_states, w, ids, experts, clamp_limit=clamp_limit)
