@@ -1,20 +1,23 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized-linear hot path on one MI355X.
 
-Workload: the int4 W4A16 group-128 decode sweep at
-Llama-3-8B MLP shapes -- gate_up (K=4096, N=28672) and down (K=14336, N=4096),
-M in {1, 8, 32, 128}, bf16 activations ~ N(0,1), codes ~ U{0..15}, zero point
-8, bf16 scales ~ U[0.002, 0.02].  One *step* is one pass over the sweep: the 8
-GEMMs (2 shapes x 4 M), each on the next of a rotating set of weight copies
-(>= 512 MB per shape, twice the 256 MB Infinity Cache) so bytes come from HBM.
+Headline workload: the int4 W4A16 group-128 decode
+sweep at Llama-3-8B MLP shapes -- gate_up (K=4096, N=28672) and down (K=14336,
+N=4096), M in {1, 8, 32, 128}, bf16 activations ~ N(0,1), codes ~ U{0..15}, zero
+point 8, bf16 scales ~ U[0.002, 0.02].  One *step* is one pass over the sweep:
+the 8 GEMMs, each on the next of a rotating set of weight copies (>= 512 MiB per
+shape, twice the 256 MiB Infinity Cache) so bytes come from HBM.  ``value`` is
+HBM GB/s over the packed-weight + scale bytes of a step (the config's unit).
 
-``value`` is HBM GB/s over the packed-weight + scale bytes of the step (the
-config's stated unit).  ``roofline`` describes the dominant HBM-bound launch,
-gate_up at M=32, with bytes = weights + scales + activations + output, timed
-with HIP events on the stream the kernel runs on.  ``cpu_baseline`` times the
-CPU oracle (dequantize-then-matmul, oracle/int4.py) on one gate_up M=32 GEMM.
+``roofline`` describes the launch that dominates a step's time, with its
+algorithmic bytes (or flops) over its average duration, measured with HIP
+events on the stream the kernel runs on.  ``points`` lists every BASELINE
+config measured the same way: config 0 (int4 fp16), config 2 (FP8 per-token x
+per-channel, Llama-3-70B), config 3 (DeepSeek 128x128 block FP8) and config 4
+(routed FP8 MoE, 256 experts, top-8, router included).  ``cpu_baseline`` times
+the CPU oracle (dequantize-then-matmul, oracle/int4.py) on one gate_up M=32 GEMM.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only int4|fp8|moe]
 """
 from __future__ import annotations
 
@@ -30,10 +33,15 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
 ROTATE_BYTES = 512 * 2**20
 SHAPES = {"gate_up": (4096, 28672), "down": (14336, 4096)}
 MS = (1, 8, 32, 128)
-HEADLINE = ("gate_up", 32)
+FP8_SHAPES = {"qkv": (8192, 10240), "gate_up": (8192, 57344), "down": (28672, 8192)}
+FP8_MS = (1, 64, 512, 4096)
+BLOCK_SHAPES = {"a": (7168, 18432), "b": (18432, 7168), "c": (7168, 24576)}
+BLOCK_MS = (16, 256, 4096)
+MOE_TS = (64, 512, 4096)
 
 
 def log(*a):
@@ -80,57 +88,10 @@ def cpu_baseline(seconds_budget: float = 20.0) -> dict:
     }
 
 
-class Int4Point:
-    def __init__(self, name, k, n, m, dev, copies):
-        import torch
-        from torchinferno_amd import _lib
-        from torchinferno_amd.kernels import int4 as ti4
-        self.name, self.k, self.n, self.m = name, k, n, m
-        self.a = torch.randn((m, k), device=dev, dtype=torch.bfloat16)
-        self.out = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
-        self.copies = copies
-        self.ws = ti4.make_workspace(n, dev, size_k=k, max_m=m)
-        self.fn = _lib.lib().ti_w4a16_gemm
-        self.ws_bytes = self.ws.numel() * 4
-        self.i = 0
-
-    def launch(self, stream):
-        pw, ps = self.copies[self.i % len(self.copies)]
-        self.i += 1
-        st = self.fn(self.a.data_ptr(), 2, pw.data_ptr(), ps.data_ptr(), self.out.data_ptr(),
-                     self.m, self.n, self.k, 128, self.ws.data_ptr(), self.ws_bytes, stream)
-        if st:
-            raise RuntimeError(f"ti_w4a16_gemm failed: {st}")
-
-    @property
-    def wbytes(self):
-        return weight_bytes(self.k, self.n)
-
-    @property
-    def algo_bytes(self):
-        return self.wbytes + self.m * self.k * 2 + self.m * self.n * 2
-
-    @property
-    def flops(self):
-        return 2 * self.m * self.n * self.k
-
-
-def make_copies(k, n, dev):
-    import torch
-    from torchinferno_amd.kernels import int4 as ti4
-    codes = torch.randint(0, 16, (k, n), device=dev, dtype=torch.int32)
-    q = ti4.pack_int4(codes)
-    del codes
-    s = (torch.rand((k // 128, n), device=dev) * 0.018 + 0.002).to(torch.bfloat16)
-    ncopy = max(2, -(-ROTATE_BYTES // weight_bytes(k, n)))
-    copies = [ti4.repack_int4(q, s) for _ in range(ncopy)]
-    torch.cuda.synchronize()
-    return copies
-
-
 def timed_burst(launch_fns, reps, stream_handle):
     """Queue `reps` rounds of launches behind a spin kernel so the host never
-    starves the GPU; return elapsed GPU ms between the events."""
+    starves the GPU; return elapsed GPU ms between events recorded on the
+    launches' stream."""
     import torch
     torch.cuda._sleep(int(50e6))
     start = torch.cuda.Event(enable_timing=True)
@@ -144,12 +105,189 @@ def timed_burst(launch_fns, reps, stream_handle):
     return start.elapsed_time(end)
 
 
+def _check(name, st):
+    if st:
+        from torchinferno_amd import _lib
+        raise RuntimeError(f"{name} failed ({st}): {_lib.lib().ti_last_error().decode()}")
+
+
+# --------------------------------------------------------------------------- int4
+
+
+class Int4Point:
+    def __init__(self, name, k, n, m, dev, copies, dtype_code=2):
+        import torch
+        from torchinferno_amd import _lib
+        from torchinferno_amd.kernels import int4 as ti4
+        self.name, self.k, self.n, self.m = name, k, n, m
+        dt = torch.bfloat16 if dtype_code == 2 else torch.float16
+        self.dtype_code = dtype_code
+        self.a = torch.randn((m, k), device=dev, dtype=dt)
+        self.out = torch.empty((m, n), device=dev, dtype=dt)
+        self.copies = copies
+        self.ws = ti4.make_workspace(n, dev, size_k=k, max_m=m)
+        self.fn = _lib.lib().ti_w4a16_gemm
+        self.ws_bytes = self.ws.numel() * 4
+        self.i = 0
+
+    def launch(self, stream):
+        pw, ps = self.copies[self.i % len(self.copies)]
+        self.i += 1
+        _check("ti_w4a16_gemm", self.fn(self.a.data_ptr(), self.dtype_code, pw.data_ptr(), ps.data_ptr(),
+                                        self.out.data_ptr(), self.m, self.n, self.k, 128, self.ws.data_ptr(),
+                                        self.ws_bytes, stream))
+
+    @property
+    def wbytes(self):
+        return weight_bytes(self.k, self.n)
+
+    @property
+    def algo_bytes(self):
+        return self.wbytes + self.m * self.k * 2 + self.m * self.n * 2
+
+    @property
+    def flops(self):
+        return 2 * self.m * self.n * self.k
+
+    @property
+    def bound(self):
+        # bf16 ridge: 2.5 PFLOP/s / 8 TB/s = 312 flop/byte
+        return "mfma" if self.flops / self.algo_bytes > BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
+
+
+def make_int4_copies(k, n, dev, dtype=None):
+    import torch
+    from torchinferno_amd.kernels import int4 as ti4
+    dtype = dtype or torch.bfloat16
+    codes = torch.randint(0, 16, (k, n), device=dev, dtype=torch.int32)
+    q = ti4.pack_int4(codes)
+    del codes
+    s = (torch.rand((k // 128, n), device=dev) * 0.018 + 0.002).to(dtype)
+    ncopy = max(2, -(-ROTATE_BYTES // weight_bytes(k, n)))
+    copies = [ti4.repack_int4(q, s) for _ in range(ncopy)]
+    torch.cuda.synchronize()
+    return copies
+
+
+def point_record(label, t_s, algo_bytes, flops, bound, peak_tf, extra=None):
+    gbs = algo_bytes / t_s / 1e9
+    tf = flops / t_s / 1e12
+    rec = {"point": label, "us": round(t_s * 1e6, 2), "algo_GBs": round(gbs, 1), "TFLOPs": round(tf, 2),
+           "bound": bound, "frac": round(gbs / HBM_PEAK_GBS if bound == "hbm" else tf / peak_tf, 4)}
+    if extra:
+        rec.update(extra)
+    return rec
+
+
+# --------------------------------------------------------------------------- FP8
+
+
+def fp8_points(dev, stream):
+    """Config 2 (rowcol) and config 3 (block) GEMMs, excluding activation quant."""
+    import torch
+    from torchinferno_amd import _lib
+    L = _lib.lib()
+    ws = torch.zeros(64 << 20, dtype=torch.int32, device=dev)
+    recs = []
+    for mode, shapes, ms in ((0, FP8_SHAPES, FP8_MS), (1, BLOCK_SHAPES, BLOCK_MS)):
+        for sname, (k, n) in shapes.items():
+            ncopy = max(2, -(-ROTATE_BYTES // (n * k)))
+            bq = [torch.randint(-120, 120, (n, k), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
+                  for _ in range(ncopy)]
+            bs = [torch.rand((n,) if mode == 0 else (-(-n // 128), k // 128), device=dev) * 1e-3 + 1e-4
+                  for _ in range(ncopy)]
+            for m in ms:
+                a = torch.randint(-120, 120, (m, k), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
+                asc = torch.rand((m,) if mode == 0 else (m, k // 128), device=dev) * 0.01 + 1e-3
+                out = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
+                i = [0]
+
+                def launch(st, a=a, asc=asc, out=out, m=m, k=k, n=n, i=i, bq=bq, bs=bs, mode=mode):
+                    j = i[0] % len(bq)
+                    i[0] += 1
+                    if mode == 0:
+                        r = L.ti_fp8_gemm_rowcol(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(),
+                                                 1, out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
+                    else:
+                        r = L.ti_fp8_gemm_block(a.data_ptr(), asc.data_ptr(), bq[j].data_ptr(), bs[j].data_ptr(),
+                                                out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
+                    _check("fp8 gemm", r)
+
+                reps = 10 if m >= 4096 else 40
+                timed_burst([launch], 3, stream)
+                t = timed_burst([launch], reps, stream) / reps * 1e-3
+                flops = 2 * m * n * k
+                scale_bytes = n * 4 if mode == 0 else (-(-n // 128)) * (k // 128) * 4
+                algo = n * k + scale_bytes + m * k + m * n * 2
+                bound = "mfma" if flops / algo > FP8_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
+                cfg = "config2" if mode == 0 else "config3"
+                recs.append(point_record(f"{cfg} fp8 {'rowcol' if mode == 0 else 'block'} {sname} M={m} K={k} N={n}",
+                                         t, algo, flops, bound, FP8_PEAK_TFLOPS))
+                log(recs[-1])
+            del bq, bs
+            torch.cuda.empty_cache()
+    return recs
+
+
+# --------------------------------------------------------------------------- MoE
+
+
+def moe_points(dev, stream):
+    """Config 4: router + routed experts (256 experts, H=7168, I=2048, top-8)."""
+    import torch
+    from torchinferno_amd import _lib
+    from torchinferno_amd.kernels import moe as tmoe
+    L = _lib.lib()
+    e, h, inter, k = 256, 7168, 2048, 8
+    w13 = torch.randint(-120, 120, (e, 2 * inter, h), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
+    w2 = torch.randint(-120, 120, (e, h, inter), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
+    s13 = torch.rand((e, 2 * inter // 128, h // 128), device=dev) * 1e-3 + 1e-4
+    s2 = torch.rand((e, h // 128, inter // 128), device=dev) * 1e-3 + 1e-4
+    recs = []
+    per_expert = 2 * inter * h + h * inter + (s13[0].numel() + s2[0].numel()) * 4
+    for t in MOE_TS:
+        g = torch.Generator(device=dev).manual_seed(t)
+        x = torch.randn((t, h), generator=g, device=dev).to(torch.bfloat16)
+        logits = torch.randn((t, e), generator=g, device=dev)
+        wts = torch.empty((t, k), dtype=torch.float32, device=dev)
+        ids = torch.empty((t, k), dtype=torch.int32, device=dev)
+        out = torch.empty((t, h), dtype=torch.bfloat16, device=dev)
+        need = int(L.ti_fp8_moe_workspace_bytes(t, k, e, h, inter))
+        ws = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+        wsp = (ws.data_ptr() + 255) & ~255
+
+        def launch(st, t=t, x=x, logits=logits, wts=wts, ids=ids, out=out, wsp=wsp, need=need):
+            _check("route", L.ti_moe_route_topk(logits.data_ptr(), t, e, k, 1, 1.0, wts.data_ptr(), ids.data_ptr(), st))
+            _check("moe", L.ti_fp8_moe(x.data_ptr(), wts.data_ptr(), ids.data_ptr(), t, k, w13.data_ptr(),
+                                       s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), e, h, inter, 0.0,
+                                       out.data_ptr(), wsp, need, st))
+
+        timed_burst([launch], 2, stream)
+        reps = 10
+        ms = timed_burst([launch], reps, stream) / reps
+        torch.cuda.synchronize()
+        touched = int(torch.unique(ids).numel())
+        algo = touched * per_expert + t * h * 2 * 2
+        flops = t * k * 2 * (2 * inter * h + h * inter)
+        recs.append(point_record(f"config4 fp8 moe T={t} experts_touched={touched}", ms * 1e-3, algo, flops, "hbm",
+                                 FP8_PEAK_TFLOPS))
+        log(recs[-1])
+    del w13, w2
+    torch.cuda.empty_cache()
+    return recs
+
+
+# --------------------------------------------------------------------------- main
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["int4", "fp8", "moe"], default=None,
+                    help="run only one family of points (profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -166,22 +304,39 @@ def main():
     torch.manual_seed(0)
     props = torch.cuda.get_device_properties(dev)
     log(f"device: {props.name} CUs={props.multi_processor_count}")
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    extra_points = []
+    if args.only in (None, "fp8"):
+        extra_points += fp8_points(dev, stream)
+    if args.only in (None, "moe"):
+        extra_points += moe_points(dev, stream)
+    if args.only in ("fp8", "moe"):
+        print(json.dumps({"points": extra_points}), flush=True)
+        return
+
+    # config 0: fp16 M=16 K=N=4096
+    c0 = make_int4_copies(4096, 4096, dev, torch.float16)
+    p0 = Int4Point("config0", 4096, 4096, 16, dev, c0, dtype_code=1)
+    timed_burst([p0.launch], 20, stream)
+    t0 = timed_burst([p0.launch], 200, stream) / 200 * 1e-3
+    extra_points.insert(0, point_record("config0 int4 fp16 M=16 K=4096 N=4096", t0, p0.algo_bytes, p0.flops,
+                                        p0.bound, BF16_PEAK_TFLOPS))
+    del c0, p0
 
     points = []
     for name, (k, n) in SHAPES.items():
-        copies = make_copies(k, n, dev)
+        copies = make_int4_copies(k, n, dev)
         log(f"{name}: K={k} N={n} copies={len(copies)}")
         for m in MS:
             points.append(Int4Point(name, k, n, m, dev, copies))
-    stream = torch.cuda.current_stream(dev).cuda_stream
 
     # Per-point launch durations (each point alone, back-to-back launches).
     per_point = {}
     for p in points:
         timed_burst([p.launch], 20, stream)  # warm
         reps = 200
-        ms = timed_burst([p.launch], reps, stream)
-        per_point[(p.name, p.m)] = ms / reps
+        per_point[(p.name, p.m)] = timed_burst([p.launch], reps, stream) / reps
 
     # The timed region: exactly `steps` steps of the full sweep.
     for _ in range(args.warmup):
@@ -192,14 +347,14 @@ def main():
     torch.cuda._sleep(int(50e6))
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
+    t_wall = time.perf_counter()
     start.record()
     for _ in range(args.steps):
         for fn in launches:
             fn(stream)
     end.record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    wall = time.perf_counter() - t_wall
     gpu_ms = start.elapsed_time(end)
     ms_per_step = gpu_ms / args.steps
     step_bytes = sum(p.wbytes for p in points)
@@ -208,25 +363,23 @@ def main():
     pts = []
     for p in points:
         t = per_point[(p.name, p.m)] * 1e-3
-        gbs = p.algo_bytes / t / 1e9
-        tf = p.flops / t / 1e12
-        hbm_bound = p.m <= 32
-        pts.append({
-            "shape": p.name, "M": p.m, "K": p.k, "N": p.n, "us": round(t * 1e6, 2),
-            "weight_GBs": round(p.wbytes / t / 1e9, 1), "algo_GBs": round(gbs, 1),
-            "TFLOPs": round(tf, 2), "bound": "hbm" if hbm_bound else "mfma",
-            "frac": round(gbs / HBM_PEAK_GBS if hbm_bound else tf / BF16_PEAK_TFLOPS, 4),
-        })
-    head = next(p for p in points if (p.name, p.m) == HEADLINE)
-    t_head = per_point[HEADLINE] * 1e-3
-    achieved = head.algo_bytes / t_head / 1e9
+        pts.append(point_record(f"config1 int4 bf16 {p.name} M={p.m} K={p.k} N={p.n}", t, p.algo_bytes, p.flops,
+                                p.bound, BF16_PEAK_TFLOPS, {"weight_GBs": round(p.wbytes / t / 1e9, 1)}))
+    # Dominant launch of the step: the largest share of its time.
+    dom = max(points, key=lambda p: per_point[(p.name, p.m)])
+    t_dom = per_point[(dom.name, dom.m)] * 1e-3
+    if dom.bound == "hbm":
+        achieved, peak, unit = dom.algo_bytes / t_dom / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved, peak, unit = dom.flops / t_dom / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
     roofline = {
-        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-        "kernel": "ti::int4::w4a16_decode_kernel<bf16, MR=32, NT=4, WK=2, R=3, SPLIT=0>",
-        "launch": "gate_up K=4096 N=28672 M=32",
-        "avg_launch_us": round(t_head * 1e6, 2),
-        "algo_bytes_per_launch": head.algo_bytes,
+        "bound": dom.bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
+        "frac": round(achieved / peak, 4), "traffic": None,
+        "kernel": "ti::int4 W4A16 GEMM (ti_w4a16_gemm)",
+        "launch": f"{dom.name} K={dom.k} N={dom.n} M={dom.m}",
+        "avg_launch_us": round(t_dom * 1e6, 2),
+        "algo_bytes_per_launch": dom.algo_bytes, "flops_per_launch": dom.flops,
+        "share_of_step": round(t_dom * 1e3 / ms_per_step, 3),
     }
     cpu = None
     if not args.no_cpu_baseline:
@@ -244,13 +397,13 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (random int4 codes, bf16 scales/activations; no checkpoint)",
+        "data": "synthetic (random int4 codes, bf16 scales/activations; random e4m3 codes for FP8; no checkpoint)",
         "config": {"workload": "int4 W4A16 g128 decode sweep (BASELINE configs[1])",
                    "shapes": {k: {"K": v[0], "N": v[1]} for k, v in SHAPES.items()},
                    "M": list(MS), "bytes_per_step": step_bytes, "parallelism": "none (1 GPU)"},
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "points": pts,
+        "points": pts + extra_points,
         "wall_s": round(wall, 3),
     }
     print(json.dumps(line), flush=True)

@@ -65,6 +65,16 @@ int ti_int4_repack(const int32_t* qweight, const void* scales, int scale_dtype,
                    int K, int N, int group_size,
                    int32_t* packed_weight, void* packed_scales, hipStream_t stream);
 
+/* Symmetric round-to-nearest int4 quantization of a [K, N] fp16/bf16 weight
+ * (K-major: the reference passes weight.t()) into the canonical layout:
+ * per (128-row group, column) w is rounded to fp16, s = max(|max/7|, |min/-8|)
+ * clamped >= 1e-8 (fp32), q = clamp(rint(w/s), -8, 7) + 8, scales stored in
+ * scale_dtype.  Replaces the quantizer of quantize_to_marlin_int4
+ * (src/torchinferno/kernels/marlin.py:117-128); bit-identical to the same
+ * formula evaluated with IEEE fp32 division on the host. */
+int ti_int4_quantize_rtn(const void* weight_kn, int weight_dtype, int K, int N, int group_size,
+                         int scale_dtype, int32_t* qweight, void* scales, hipStream_t stream);
+
 /* Dequantize a kernel-layout weight to fp32 [K, N]: out = (q - 8) * s, exact.
  * Shares the in-register unpack of ti_w4a16_gemm (bit-exactness check). */
 int ti_int4_dequant(const int32_t* packed_weight, const void* packed_scales, int scale_dtype,

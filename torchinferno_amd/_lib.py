@@ -36,6 +36,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ti_int4_packed_scale_bytes": (_sz, [_i, _i, _i]),
     "ti_int4_repack": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp]),
     "ti_int4_dequant": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp]),
+    "ti_int4_quantize_rtn": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
     "ti_w4a16_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "ti_w4a16_workspace_bytes_max": (_sz, [_i, _i, _i, _i]),
     "ti_w4a16_gemm": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),

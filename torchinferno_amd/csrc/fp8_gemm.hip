@@ -440,7 +440,11 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   // scales favour it from 128 tiles -- then 128x128, split over K below 128).
   auto tiles = [&](int bm, int bn) { return (long)cdiv(M, bm) * cdiv(N, bn); };
   int splits = 1;
-  if (M <= 64) {
+  if (M <= 4) {
+    p.kind = 3;
+    const long t = tiles(16, 256);
+    splits = t >= 128 ? 1 : (int)(cdiv(256, (int)t) < 4 ? cdiv(256, (int)t) : 4);
+  } else if (M <= 64) {
     p.kind = M <= 16 ? 6 : 5;
     const long t = tiles(kBM[p.kind], kBN[p.kind]);
     splits = t >= 72 ? 1 : (int)(cdiv(256, (int)t) < 4 ? cdiv(256, (int)t) : 4);

@@ -67,6 +67,46 @@ __global__ void repack_weight_kernel(const uint32_t* __restrict__ q, uint32_t* _
   out[idx] = interleave_nibbles(q[krow * N + t * 16 + c]);
 }
 
+// Symmetric RTN int4 quantization of a [K, N] weight into the canonical
+// layout: the quantizer of src/torchinferno/kernels/marlin.py:117-128.  Per
+// (128-row group, column): w is first rounded to fp16 (as the reference casts
+// the weight), s = max(|max/7|, |min/-8|) clamped >= 1e-8 in fp32 (IEEE
+// division), q = clamp(rint(w / s), -8, 7) + 8 (round half to even), scales
+// stored RNE in the scale dtype.  One thread per (group, column).
+template <int WDT, int SDT>
+__global__ void quantize_rtn_kernel(const uint16_t* __restrict__ w, int K, int N,
+                                    uint32_t* __restrict__ q, uint16_t* __restrict__ s) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int NG = K / kGroup;
+  if (idx >= (long)NG * N) return;
+  const int n = (int)(idx % N);
+  const int g = (int)(idx / N);
+  const uint16_t* col = w + (long)g * kGroup * N + n;
+  float v[kGroup];
+  float mx = -INFINITY, mn = INFINITY;
+#pragma unroll 8
+  for (int i = 0; i < kGroup; ++i) {
+    const float f = WDT == TI_DTYPE_F16 ? f16_bits_to_f32(col[(long)i * N]) : bf16_bits_to_f32(col[(long)i * N]);
+    v[i] = (float)(_Float16)f;  // round to fp16 (subnormals kept)
+    mx = fmaxf(mx, v[i]);
+    mn = fminf(mn, v[i]);
+  }
+  float sc = fmaxf(fabsf(mx / 7.0f), fabsf(mn / -8.0f));
+  sc = fmaxf(sc, 1e-8f);
+#pragma unroll
+  for (int r = 0; r < kGroup / 8; ++r) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float c = __builtin_rintf(v[r * 8 + e] / sc);
+      c = fminf(fmaxf(c, -8.0f), 7.0f);
+      word |= (uint32_t)((int)c + 8) << (4 * e);
+    }
+    q[((long)g * (kGroup / 8) + r) * N + n] = word;
+  }
+  s[(long)g * N + n] = SDT == TI_DTYPE_F16 ? f32_to_f16_bits(sc) : f32_to_bf16_bits(sc);
+}
+
 // Exact dequant of the block layout, through the same unpack8: one wave per block.
 template <int DT>
 __global__ void dequant_kernel(const i32x4* __restrict__ wp, const uint16_t* __restrict__ sp,
@@ -439,6 +479,29 @@ extern "C" int ti_int4_repack(const int32_t* qweight, const void* scales, int sc
     set_error("ti_int4_repack: scale copy failed: %s", hipGetErrorString(e));
     return TI_ERR_HIP;
   }
+  return TI_OK;
+}
+
+extern "C" int ti_int4_quantize_rtn(const void* weight_kn, int weight_dtype, int K, int N, int group_size,
+                                    int scale_dtype, int32_t* qweight, void* scales, hipStream_t stream) {
+  TI_CHECK_ARG(weight_kn && qweight && scales, "ti_int4_quantize_rtn: null pointer");
+  TI_CHECK_ARG((weight_dtype == TI_DTYPE_F16 || weight_dtype == TI_DTYPE_BF16) &&
+                   (scale_dtype == TI_DTYPE_F16 || scale_dtype == TI_DTYPE_BF16),
+               "ti_int4_quantize_rtn: weight and scale dtypes must be fp16 or bf16");
+  TI_CHECK_SHAPE(group_size == kGroup, "ti_int4_quantize_rtn: group_size must be 128 (got %d)", group_size);
+  TI_CHECK_SHAPE(K > 0 && N > 0 && K % kGroup == 0, "ti_int4_quantize_rtn: need K %% 128 == 0 (K=%d)", K);
+  const long total = (long)(K / kGroup) * N;
+  dim3 grid((unsigned)((total + 255) / 256));
+#define TI_QR(W, S)                                                                                       \
+  hipLaunchKernelGGL((quantize_rtn_kernel<W, S>), grid, dim3(256), 0, stream, (const uint16_t*)weight_kn, K, N, \
+                     (uint32_t*)qweight, (uint16_t*)scales)
+  if (weight_dtype == TI_DTYPE_F16) {
+    if (scale_dtype == TI_DTYPE_F16) TI_QR(TI_DTYPE_F16, TI_DTYPE_F16); else TI_QR(TI_DTYPE_F16, TI_DTYPE_BF16);
+  } else {
+    if (scale_dtype == TI_DTYPE_F16) TI_QR(TI_DTYPE_BF16, TI_DTYPE_F16); else TI_QR(TI_DTYPE_BF16, TI_DTYPE_BF16);
+  }
+#undef TI_QR
+  TI_CHECK_LAUNCH("ti_int4_quantize_rtn");
   return TI_OK;
 }
 

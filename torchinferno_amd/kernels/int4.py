@@ -52,13 +52,26 @@ def pack_int4(codes_kn: Tensor) -> Tensor:
 def quantize_int4_rtn(weight_kn: Tensor, group_size: int = GROUP_SIZE,
                       scale_dtype: torch.dtype = torch.bfloat16) -> tuple[Tensor, Tensor]:
     """Symmetric round-to-nearest int4, the quantizer of marlin.py:117-128, producing
-    the canonical layout: (qweight int32 [K/8, N], scales [K/G, N] in scale_dtype)."""
+    the canonical layout: (qweight int32 [K/8, N], scales [K/G, N] in scale_dtype).
+
+    GPU tensors run the ``ti_int4_quantize_rtn`` kernel (IEEE fp32 division, round
+    half to even -- bit-identical to the host formula); host tensors (weight
+    preparation off the GPU) run the same formula in torch on the CPU."""
     if weight_kn.ndim != 2:
         raise ValueError("weight must be [K, N]")
-    w = weight_kn.to(torch.float16).float()
-    k, n = w.shape
+    k, n = weight_kn.shape
     if k % group_size:
         raise ValueError("K must be a multiple of group_size")
+    if weight_kn.device.type == "cuda":
+        if weight_kn.dtype not in _SCALE_DTYPES or scale_dtype not in _SCALE_DTYPES:
+            raise ValueError("weight and scale dtypes must be fp16 or bf16")
+        wc = weight_kn.contiguous()
+        q = torch.empty((k // 8, n), dtype=torch.int32, device=wc.device)
+        s = torch.empty((k // group_size, n), dtype=scale_dtype, device=wc.device)
+        _lib.call("ti_int4_quantize_rtn", wc.data_ptr(), _lib.dtype_code(wc.dtype), k, n, group_size,
+                  _lib.dtype_code(scale_dtype), q.data_ptr(), s.data_ptr(), _lib.stream_of(wc))
+        return q, s
+    w = weight_kn.to(torch.float16).float()
     g = w.reshape(k // group_size, group_size, n)
     mx = g.amax(dim=1)
     mn = g.amin(dim=1)
@@ -111,12 +124,33 @@ def workspace_bytes(size_m: int, size_n: int, size_k: int, group_size: int = GRO
     return int(_lib.lib().ti_w4a16_workspace_bytes(size_m, size_n, size_k, group_size))
 
 
-def make_workspace(size_n: int, device, *, size_k: int, max_m: int = 128,
+def make_workspace(size_n: int, device, *, size_k: int | None = None, max_m: int = 128,
                    group_size: int = GROUP_SIZE) -> Tensor:
     """Zero-filled workspace serving every M in [1, max_m] for an [K, N] weight.
-    Kernels leave it zeroed; calls sharing it must be ordered on one stream."""
+    Kernels leave it zeroed; calls sharing it must be ordered on one stream.
+
+    Called as the reference calls Marlin's (``make_workspace(n, device)``,
+    marlin.py:134-136) -- without ``size_k`` -- it returns a minimal buffer, and
+    ``int4_mm`` then uses a per-device shared workspace that grows on demand (do a
+    first call at the largest M before capturing graphs)."""
+    if size_k is None:
+        return torch.zeros(4, dtype=torch.int32, device=device)
     need = int(_lib.lib().ti_w4a16_workspace_bytes_max(max_m, size_n, size_k, group_size))
     return torch.zeros(max(4, (need + 3) // 4), dtype=torch.int32, device=device)
+
+
+_shared_ws: dict[int, Tensor] = {}
+
+
+def _shared_workspace(device: torch.device, nbytes: int) -> Tensor:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _shared_ws.get(idx)
+    if ws is None or ws.numel() * 4 < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("int4 workspace must be sized before graph capture (run the largest M once)")
+        ws = torch.zeros((nbytes + 3) // 4, dtype=torch.int32, device=device)
+        _shared_ws[idx] = ws
+    return ws
 
 
 def int4_mm(a: Tensor, q_weight: Tensor, scales: Tensor, workspace: Tensor, size_n: int,
@@ -143,10 +177,14 @@ def int4_mm(a: Tensor, q_weight: Tensor, scales: Tensor, workspace: Tensor, size
     _lib.require_device(a, q_weight, scales)
     if q_weight.numel() * 8 != size_k * size_n:
         raise ValueError("q_weight does not hold a [size_k, size_n] int4 weight")
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    need = workspace_bytes(m, size_n, size_k)
+    if need > ws_bytes:
+        workspace = _shared_workspace(a.device, need)
+        ws_bytes = workspace.numel() * 4
     _lib.call("ti_w4a16_gemm", a.data_ptr(), _lib.dtype_code(a.dtype), q_weight.data_ptr(),
               scales.data_ptr(), out.data_ptr(), m, size_n, size_k, GROUP_SIZE,
-              _lib.ptr(workspace), 0 if workspace is None else workspace.numel() * workspace.element_size(),
-              _lib.stream_of(a))
+              _lib.ptr(workspace), ws_bytes, _lib.stream_of(a))
     return out
 
 
