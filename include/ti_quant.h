@@ -87,6 +87,11 @@ int ti_int4_dequant(const int32_t* packed_weight, const void* packed_scales, int
 size_t ti_w4a16_workspace_bytes(int M, int N, int K, int group_size);
 size_t ti_w4a16_workspace_bytes_max(int max_m, int N, int K, int group_size);
 
+/* Name and parameters of the kernel plan ti_w4a16_gemm would launch for this
+ * problem, written to buf (introspection and tuning; no counterpart in the
+ * reference).  Returns TI_ERR_UNSUPPORTED if no valid plan exists. */
+int ti_w4a16_plan_name(int M, int N, int K, int group_size, char* buf, size_t len);
+
 /* out[M, N] = a[M, K] @ dequant(W), fp32 accumulation, out in a's dtype.
  * Replaces torch.ops._C.marlin_gemm as called by marlin_int4_mm
  * (src/torchinferno/kernels/marlin.py:142-171).  dtype: TI_DTYPE_F16 or

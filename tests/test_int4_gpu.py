@@ -165,5 +165,23 @@ def test_decode_kernel_plans(dev, monkeypatch, plan, m):
     print(f"[int4] decode plan {plan} M={m}", flush=True)
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MIN_M", "1")
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_PLAN", plan)
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MR", "4" if m <= 4 else ("16" if m <= 16 else "32"))
     out, ref = _run_gemm(dev, m, 2048, 512, torch.float16 if m % 2 else torch.bfloat16, 20 + m)
+    assert _rel_err(out.float().cpu().numpy(), ref) <= TOL
+
+
+# Tall tiles (64 / 128 staged rows): each instantiated (nt, wk, ring) with and
+# without split-K, ragged M, both activation dtypes.
+_TALL_PLANS = ["2:2:2:1", "4:1:2:1", "4:1:3:2", "2:1:3:1", "2:1:4:3"]
+
+
+@pytest.mark.parametrize("plan", _TALL_PLANS)
+@pytest.mark.parametrize("mr,m", [(64, 40), (64, 100), (128, 77), (128, 128), (128, 200)])
+def test_decode_kernel_tall_tiles(dev, monkeypatch, plan, mr, m):
+    print(f"[int4] tall plan {plan} MR={mr} M={m}", flush=True)
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MIN_M", "1")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MAX_M", "4096")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MR", str(mr))
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_PLAN", plan)
+    out, ref = _run_gemm(dev, m, 2048, 512, torch.float16 if m % 2 else torch.bfloat16, 30 + m)
     assert _rel_err(out.float().cpu().numpy(), ref) <= TOL

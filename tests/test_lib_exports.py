@@ -46,3 +46,28 @@ def test_gemm_rejects_bad_arguments_without_gpu():
     assert b"null" in lib.ti_last_error()
     st = lib.ti_w4a16_gemm(16, 2, 16, 16, 16, 1, 100, 128, 128, None, 0, None)
     assert st == _lib.TI_ERR_UNSUPPORTED
+
+
+def test_every_int4_plan_is_launchable(monkeypatch):
+    """Host-side plan selection names an instantiated kernel whose workgroups tile N
+    exactly, for every M and every N granularity, under the tuning overrides too."""
+    import ctypes
+    lib = _lib.lib()
+    buf = ctypes.create_string_buffer(256)
+    cases = [(k, n) for k in (128, 1024, 4096, 14336) for n in (64, 192, 320, 512, 4096, 28672)]
+    for mr in (None, "4", "16", "32", "64", "128"):
+        for plan in (None, "1:1:3:1", "4:4:6:8", "2:2:2:1", "4:1:2:2"):
+            if mr:
+                monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MR", mr)
+            else:
+                monkeypatch.delenv("TI_ROCM_W4A16_DECODE_MR", raising=False)
+            if plan:
+                monkeypatch.setenv("TI_ROCM_W4A16_DECODE_PLAN", plan)
+            else:
+                monkeypatch.delenv("TI_ROCM_W4A16_DECODE_PLAN", raising=False)
+            monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MIN_M", "1")
+            monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MAX_M", "4096")
+            for k, n in cases:
+                for m in (1, 3, 17, 33, 64, 65, 128, 129, 300):
+                    st = lib.ti_w4a16_plan_name(m, n, k, 128, buf, 256)
+                    assert st == 0, (mr, plan, m, n, k, lib.ti_last_error())

@@ -87,5 +87,38 @@ __device__ __forceinline__ void compute_group(const i32x4 (&w)[NT], const i32x4 
   }
 }
 
+
+// The same per-group compute for tall tiles (MT >= 4): each weight tile is
+// unpacked once, then the 16-row activation tiles are read from LDS one at a
+// time (get_a(mt, j)), so only one row tile's A operand is live at a time.
+template <int DT, int MT, int NT, typename GetA>
+__device__ __forceinline__ void compute_group_rows(const i32x4 (&w)[NT], GetA&& get_a, const float (&sc)[NT],
+                                                   f32x4 (&acc)[NT][MT]) {
+  const uint32_t mask = 0x000F000Fu, magic = Magic<DT>::kOr;
+  const i32x4 negbias = {(int)Magic<DT>::kNegBiasPair, (int)Magic<DT>::kNegBiasPair,
+                         (int)Magic<DT>::kNegBiasPair, (int)Magic<DT>::kNegBiasPair};
+  i32x4 b[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[t][j] = unpack8<DT>((uint32_t)w[t][j], mask, magic);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    i32x4 a[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = get_a(mt, j);
+    f32x4 nb = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) nb = mfma16x16x32<DT>(a[j], negbias, nb);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 cc = nb;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cc = mfma16x16x32<DT>(a[j], b[t][j], cc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[t][mt][i] = __builtin_fmaf(sc[t], cc[i], acc[t][mt][i]);
+    }
+  }
+}
 }  // namespace int4
 }  // namespace ti

@@ -7,10 +7,10 @@
 namespace ti {
 namespace int4 {
 
-constexpr int kDecodeLdsMax = 160 * 1024;  // gfx950 LDS per workgroup
+constexpr int kDecodeLdsMax = 160 * 1024 - 256;  // gfx950 LDS per workgroup, less static LDS
 
 struct DecodePlan {
-  int mr;       // activation rows staged per K range and stage (4, 16 or 32)
+  int mr;       // activation rows staged per K range and stage (4, 16, 32, 64, 128)
   int nt;       // 16-column tiles per wave
   int wk;       // waves splitting K inside the workgroup (of 4)
   int ring;     // LDS ring stages
@@ -31,6 +31,8 @@ struct DecodeArgs {
 };
 
 DecodePlan make_decode_plan(int M, int N, int K);
+// The plan names an instantiated kernel whose workgroups tile N exactly.
+bool decode_plan_valid(const DecodePlan& p, int N);
 size_t decode_ticket_bytes(const DecodePlan& p);
 size_t decode_partial_bytes(const DecodePlan& p, int M, int N);
 void launch_decode(const DecodePlan& p, int dtype, const DecodeArgs& x, hipStream_t stream);

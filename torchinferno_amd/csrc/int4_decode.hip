@@ -41,7 +41,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_decode_kernel(
     uint16_t* __restrict__ out, float* __restrict__ partial, int* __restrict__ tickets, int M, int N,
     int K, int splits) {
   constexpr int WN = kWaves / WK;
-  constexpr int MT = MR > 16 ? 2 : 1;            // 16-row MFMA tiles
+  constexpr int MT = MR > 16 ? MR / 16 : 1;      // 16-row MFMA tiles
   constexpr int MP = MT * 16;                    // rows of one row chunk
   constexpr int AI = WK * MR / 4;                // 1 KiB activation DMAs per stage (all waves)
   constexpr int AI_LO = AI / kWaves;             // ... per wave: AI_LO or AI_HI
@@ -147,25 +147,30 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_decode_kernel(
     i32x4 w[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) w[t] = *(const i32x4*)(st + (wave * NT + t) * 1024 + lane * 16);
-    i32x4 a[MT][4];
     const uint8_t* ab = st + W_BYTES + wk * A_BYTES;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      // Rows past the staged MR repeat staged ones; their outputs are not stored.
-      const int r = (mt * 16 + c) % MR;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int q = 4 * j + kq;
-        a[mt][j] = *(const i32x4*)(ab + (r * 16 + (q ^ (r & 15))) * 16);
-      }
-    }
     float sc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const float v = scale_to_f32<DT>(sS[gl * WC + (wn * NT + t) * 16 + c]);
       sc[t] = valid ? v : 0.f;
     }
-    compute_group<DT, MT, NT>(w, a, sc, acc);
+    // A operand of row tile mt, step j: row r = mt*16 + c (rows past the staged
+    // MR repeat staged ones; their outputs are not stored), chunk 4j + kq.
+    auto get_a = [&](int mt, int j) {
+      const int r = (mt * 16 + c) % MR;
+      const int q = 4 * j + kq;
+      return *(const i32x4*)(ab + (r * 16 + (q ^ (r & 15))) * 16);
+    };
+    if constexpr (MT <= 2) {
+      i32x4 a[MT][4];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[mt][j] = get_a(mt, j);
+      compute_group<DT, MT, NT>(w, a, sc, acc);
+    } else {
+      compute_group_rows<DT, MT, NT>(w, get_a, sc, acc);
+    }
   }
   // No DMA may still be writing LDS when it is reused or the workgroup ends.
   wait_vm_all();
@@ -241,7 +246,7 @@ void launch_split(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) 
 
 template <int DT, int MR, int NT, int WK>
 void launch_r(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
-  if (p.ring == 3) launch_split<DT, MR, NT, WK, 3>(p, x, stream);
+  if (p.ring <= 3) launch_split<DT, MR, NT, WK, 3>(p, x, stream);
   else if (p.ring == 4) launch_split<DT, MR, NT, WK, 4>(p, x, stream);
   else launch_split<DT, MR, NT, WK, 6>(p, x, stream);
 }
@@ -260,11 +265,27 @@ void launch_nt(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
   else launch_wk<DT, MR, 4>(p, x, stream);
 }
 
+// Tall tiles (64 / 128 staged rows) instantiate a curated set of
+// (nt, wk, ring) configurations; make_decode_plan only produces these.
+template <int DT, int MR>
+void launch_tall(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
+  if (p.wk == 2) launch_split<DT, MR, 2, 2, 2>(p, x, stream);
+  else if (p.nt == 4) {
+    if (p.ring == 2) launch_split<DT, MR, 4, 1, 2>(p, x, stream);
+    else launch_split<DT, MR, 4, 1, 3>(p, x, stream);
+  } else {
+    if (p.ring == 4) launch_split<DT, MR, 2, 1, 4>(p, x, stream);
+    else launch_split<DT, MR, 2, 1, 3>(p, x, stream);
+  }
+}
+
 template <int DT>
 void launch_mr(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
   if (p.mr == 4) launch_nt<DT, 4>(p, x, stream);
   else if (p.mr == 16) launch_nt<DT, 16>(p, x, stream);
-  else launch_nt<DT, 32>(p, x, stream);
+  else if (p.mr == 32) launch_nt<DT, 32>(p, x, stream);
+  else if (p.mr == 64) launch_tall<DT, 64>(p, x, stream);
+  else launch_tall<DT, 128>(p, x, stream);
 }
 
 int stage_bytes(int mr, int nt, int wk) { return kWaves * nt * 1024 + wk * mr * 256; }
@@ -283,43 +304,82 @@ bool env_plan(DecodePlan& p) {
 
 DecodePlan make_decode_plan(int M, int N, int K) {
   DecodePlan p;
-  p.mr = M <= 4 ? 4 : (M <= 16 ? 16 : 32);
-  p.mchunks = cdiv(M, p.mr > 16 ? 32 : 16);
-  const int NG = K / kGroup;
   const int T = N / 16;
+  const bool wide = T >= 1024;
+  // Staged rows: M's own size up to 32; beyond, 32-row chunks, except wide N
+  // above 64 rows, where 64-row tiles (half the weight re-reads) win.
+  p.mr = M <= 4 ? 4 : (M <= 16 ? 16 : (M <= 64 || !wide ? 32 : 64));
+  const char* emr = getenv("TI_ROCM_W4A16_DECODE_MR");
+  if (emr && *emr) {
+    const int v = atoi(emr);
+    if (v == 4 || v == 16 || v == 32 || v == 64 || v == 128) p.mr = v;
+  }
+  const bool tall = p.mr >= 64;
+  p.mchunks = cdiv(M, p.mr > 16 ? p.mr : 16);
+  const int NG = K / kGroup;
   if (!env_plan(p)) {
-    // Measured on MI355X at the Llama-3-8B MLP shapes (decode rows 17..64):
-    // wide N (gate_up, N=28672) streams best with no split; narrow N (down,
-    // N=4096) needs all four waves on K and a 2-way split at M <= 32.
-    const bool wide = T >= 1024;
-    p.ring = wide && M > 32 ? 4 : 3;
-    if (wide) {
-      p.nt = M <= 32 ? 4 : 2;
-      p.wk = M <= 32 ? 2 : 1;
-      p.splits = 1;
+    // Measured on MI355X at the Llama-3-8B MLP shapes, rows 17..128: wide N
+    // (gate_up, N=28672) streams with whole-K workgroups; narrow N (down,
+    // N=4096) puts all four waves on K (and a 2-way split at M <= 32).
+    p.splits = 1;
+    p.ring = 3;
+    if (tall) {
+      p.nt = 4; p.wk = 1; p.ring = 2;
+      const int blocks = max(1, cdiv(T, kWaves * p.nt)) * p.mchunks;
+      p.splits = blocks >= 192 ? 1 : cdiv(256, blocks);
+    } else if (wide) {
+      if (M <= 32) { p.nt = 4; p.wk = 2; }
+      else { p.nt = 2; p.wk = 1; p.ring = 4; }
     } else {
-      p.nt = 2;
       p.wk = 4;
+      p.nt = M <= 64 ? 2 : 4;
       const int blocks = T / (p.nt * (kWaves / p.wk));
       p.splits = (M <= 32 && blocks * p.mchunks < 256) ? 2 : 1;
     }
   }
-  if (p.nt != 1 && p.nt != 2 && p.nt != 4) p.nt = 2;
-  if (p.wk != 1 && p.wk != 2 && p.wk != 4) p.wk = 1;
-  if (p.ring != 3 && p.ring != 4 && p.ring != 6) p.ring = 4;
-  // A_INSTR >= 1: WK * MP / 16 >= 1 always holds for MP >= 16.
-  while (p.nt > 1 && N % (kWaves / p.wk * p.nt * 16)) p.nt /= 2;
-  while (p.wk < 4 && N % (kWaves / p.wk * p.nt * 16)) p.wk *= 2;
+  if (tall) {
+    // The instantiated tall configurations: (2,2,2), (4,1,2|3), (2,1,3|4); a
+    // workgroup covers 256 / 128 / 64 columns, which must divide N.
+    if (p.wk == 1 && p.nt >= 4 && N % 256) p.nt = 2;
+    if (p.wk == 1 && p.nt < 4 && N % 128) p.wk = 2;
+    if (p.wk != 1) { p.wk = 2; p.nt = 2; p.ring = 2; }
+    else if (p.nt >= 4) { p.nt = 4; p.ring = p.ring <= 2 ? 2 : 3; }
+    else { p.nt = 2; p.ring = p.ring >= 4 ? 4 : 3; }
+  } else {
+    if (p.nt != 1 && p.nt != 2 && p.nt != 4) p.nt = 2;
+    if (p.wk != 1 && p.wk != 2 && p.wk != 4) p.wk = 1;
+    if (p.ring != 3 && p.ring != 4 && p.ring != 6) p.ring = 4;
+  }
+  if (!tall) {
+    while (p.nt > 1 && N % (kWaves / p.wk * p.nt * 16)) p.nt /= 2;
+    while (p.wk < 4 && N % (kWaves / p.wk * p.nt * 16)) p.wk *= 2;
+  }
   p.nblocks = N / (kWaves / p.wk * p.nt * 16);
   p.splits = max(1, min(p.splits, max(1, NG / (2 * p.wk))));
   const int ngr = cdiv(NG, p.splits);
   const int wc = kWaves / p.wk * p.nt * 16;
   const int sbytes = cdiv(ngr * wc * 2, 256) * 256;
-  while (p.ring > 3 && p.ring * stage_bytes(p.mr, p.nt, p.wk) + sbytes > kDecodeLdsMax) p.ring = p.ring == 6 ? 4 : 3;
+  auto fits = [&](int r) { return r * stage_bytes(p.mr, p.nt, p.wk) + sbytes <= kDecodeLdsMax; };
+  if (tall) {
+    while (p.ring > 2 && !fits(p.ring)) p.ring = p.ring == 4 ? 3 : 2;
+    if (p.ring == 2 && p.nt == 2 && p.wk == 1) p.ring = 3;  // (2,1,2) is not instantiated
+  } else {
+    while (p.ring > 3 && !fits(p.ring)) p.ring = p.ring == 6 ? 4 : 3;
+  }
   const int stage = p.ring * stage_bytes(p.mr, p.nt, p.wk) + sbytes;
-  const int red = (p.wk - 1) * (kWaves / p.wk) * p.nt * (p.mr > 16 ? 2 : 1) * 256 * 4;
+  const int mt = p.mr >= 16 ? p.mr / 16 : 1;
+  const int red = (p.wk - 1) * (kWaves / p.wk) * p.nt * mt * 256 * 4;
   p.lds = stage > red ? stage : red;
   return p;
+}
+
+bool decode_plan_valid(const DecodePlan& p, int N) {
+  if (N % (kWaves / p.wk * p.nt * 16) || p.nblocks * (kWaves / p.wk * p.nt * 16) != N) return false;
+  if (p.mr >= 64)
+    return (p.nt == 2 && p.wk == 2 && p.ring == 2) || (p.nt == 4 && p.wk == 1 && (p.ring == 2 || p.ring == 3)) ||
+           (p.nt == 2 && p.wk == 1 && (p.ring == 3 || p.ring == 4));
+  return (p.nt == 1 || p.nt == 2 || p.nt == 4) && (p.wk == 1 || p.wk == 2 || p.wk == 4) &&
+         (p.ring == 3 || p.ring == 4 || p.ring == 6) && (p.mr == 4 || p.mr == 16 || p.mr == 32);
 }
 
 size_t decode_ticket_bytes(const DecodePlan& p) {

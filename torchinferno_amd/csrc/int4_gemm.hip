@@ -531,7 +531,7 @@ extern "C" int ti_int4_dequant(const int32_t* packed_weight, const void* packed_
 
 // Kernel choice by M (measured on MI355X at the Llama-3-8B MLP shapes): the
 // register-ring kernel of this file streams best for M <= 16; the LDS-DMA
-// decode kernel (int4_decode.hip) for 17 <= M <= 64; above, this file's kernel
+// decode kernel (int4_decode.hip) for 17 <= M <= 128; above, this file's kernel
 // again.  TI_ROCM_W4A16_DECODE_MIN_M / _MAX_M override the range (tuning).
 static int env_int(const char* name, int dflt) {
   const char* e = getenv(name);
@@ -539,7 +539,7 @@ static int env_int(const char* name, int dflt) {
 }
 
 static bool use_decode(int M) {
-  return M >= env_int("TI_ROCM_W4A16_DECODE_MIN_M", 17) && M <= env_int("TI_ROCM_W4A16_DECODE_MAX_M", 64);
+  return M >= env_int("TI_ROCM_W4A16_DECODE_MIN_M", 17) && M <= env_int("TI_ROCM_W4A16_DECODE_MAX_M", 128);
 }
 
 // Workspace of one call: fp32 partials [splits][M][N] from the start, ticket
@@ -560,6 +560,24 @@ static WsNeed ws_need(int M, int N, int K) {
   Plan p = make_plan(M, N, K);
   if (p.splits <= 1) return {0, 0};
   return {partial_bytes(p, M, N), ticket_bytes(p)};
+}
+
+extern "C" int ti_w4a16_plan_name(int M, int N, int K, int group_size, char* buf, size_t len) {
+  TI_CHECK_ARG(buf && len > 0, "ti_w4a16_plan_name: null buffer");
+  TI_CHECK_SHAPE(group_size == kGroup && M >= 1 && N > 0 && K > 0 && K % kGroup == 0 && N % 64 == 0,
+                 "ti_w4a16_plan_name: need M >= 1, K %% 128 == 0, N %% 64 == 0");
+  if (use_decode(M)) {
+    DecodePlan d = make_decode_plan(M, N, K);
+    snprintf(buf, len, "w4a16_decode_kernel mr=%d nt=%d wk=%d ring=%d splits=%d mchunks=%d lds=%d", d.mr, d.nt, d.wk,
+             d.ring, d.splits, d.mchunks, d.lds);
+    TI_CHECK_SHAPE(d.lds <= kDecodeLdsMax && decode_plan_valid(d, N), "ti_w4a16_plan_name: invalid plan (%s)", buf);
+  } else {
+    Plan p = make_plan(M, N, K);
+    snprintf(buf, len, "w4a16_gemm_kernel mt=%d nt=%d waves=%d depth=%d splits=%d mode=%d alds=%d lds=%d", p.mt, p.nt,
+             p.waves, p.depth, p.splits, p.mode, p.alds, p.lds);
+    TI_CHECK_SHAPE(p.lds <= 160 * 1024, "ti_w4a16_plan_name: invalid plan (%s)", buf);
+  }
+  return TI_OK;
 }
 
 extern "C" size_t ti_w4a16_workspace_bytes(int M, int N, int K, int group_size) {
@@ -656,6 +674,8 @@ extern "C" int ti_w4a16_gemm(const void* a, int dtype, const int32_t* packed_wei
   if (use_decode(M)) {
     DecodePlan d = make_decode_plan(M, N, K);
     TI_CHECK_SHAPE(d.lds <= kDecodeLdsMax, "ti_w4a16_gemm: decode plan needs %d bytes of LDS", d.lds);
+    TI_CHECK_SHAPE(decode_plan_valid(d, N), "ti_w4a16_gemm: no decode kernel for plan nt=%d wk=%d ring=%d mr=%d at N=%d",
+                   d.nt, d.wk, d.ring, d.mr, N);
     DecodeArgs x{(const uint16_t*)a, (const i32x4*)packed_weight, (const uint16_t*)packed_scales,
                  (uint16_t*)out, nullptr, nullptr, M, N, K};
     if (d.splits > 1) {
