@@ -155,6 +155,28 @@ class Int4Point:
         return "mfma" if self.flops / self.algo_bytes > BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
 
 
+def plan_name(p) -> str:
+    import ctypes
+    from torchinferno_amd import _lib
+    buf = ctypes.create_string_buffer(256)
+    _lib.lib().ti_w4a16_plan_name(p.m, p.n, p.k, 128, buf, 256)
+    return buf.value.decode()
+
+
+def read_traffic(label: str):
+    """HBM bytes per launch of `label` from the committed rocprofv3 counter summary
+    (profiles/int4_dominant_traffic.txt: FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, the
+    factors a copy kernel of known size gives); None if absent or for another launch."""
+    path = os.path.join(ROOT, "profiles", "int4_dominant_traffic.txt")
+    try:
+        vals = dict(line.split("=", 1) for line in open(path).read().split("\n") if "=" in line)
+    except OSError:
+        return None
+    if vals.get("launch", "").strip() != label:
+        return None
+    return int(float(vals["hbm_bytes_per_launch"]))
+
+
 def make_int4_copies(k, n, dev, dtype=None):
     import torch
     from torchinferno_amd.kernels import int4 as ti4
@@ -288,6 +310,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["int4", "fp8", "moe"], default=None,
                     help="run only one family of points (profiling)")
+    ap.add_argument("--point", default=None,
+                    help="NAME:M -- launch only that config-1 int4 point, --steps times (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -305,6 +329,16 @@ def main():
     props = torch.cuda.get_device_properties(dev)
     log(f"device: {props.name} CUs={props.multi_processor_count}")
     stream = torch.cuda.current_stream(dev).cuda_stream
+
+    if args.point:
+        name, m = args.point.split(":")
+        k, n = SHAPES[name]
+        p = Int4Point(name, k, n, int(m), dev, make_int4_copies(k, n, dev))
+        for _ in range(args.steps):
+            p.launch(stream)
+        torch.cuda.synchronize()
+        print(json.dumps({"point": args.point, "launches": args.steps, "plan": plan_name(p)}), flush=True)
+        return
 
     extra_points = []
     if args.only in (None, "fp8"):
@@ -372,10 +406,11 @@ def main():
         achieved, peak, unit = dom.algo_bytes / t_dom / 1e9, HBM_PEAK_GBS, "GB/s"
     else:
         achieved, peak, unit = dom.flops / t_dom / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+    dom_label = f"{dom.name}:{dom.m}"
     roofline = {
         "bound": dom.bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
-        "frac": round(achieved / peak, 4), "traffic": None,
-        "kernel": "ti::int4 W4A16 GEMM (ti_w4a16_gemm)",
+        "frac": round(achieved / peak, 4), "traffic": read_traffic(dom_label),
+        "kernel": plan_name(dom),
         "launch": f"{dom.name} K={dom.k} N={dom.n} M={dom.m}",
         "avg_launch_us": round(t_dom * 1e6, 2),
         "algo_bytes_per_launch": dom.algo_bytes, "flops_per_launch": dom.flops,
