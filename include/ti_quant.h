@@ -131,6 +131,31 @@ int ti_fp8_quant_tensor(const void* x, int x_dtype, long n, const float* inv_sca
                         uint8_t* xq, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Fused activation -> per-token e4m3 producers (the step before the W8A8 GEMM).
+ * Rows of n elements (n % 8 == 0); outputs xq [rows, n] e4m3 and xs [rows]
+ * fp32 with xs = max(amax/448, 1e-10) over the activation-dtype-rounded row.
+ * The reduction and transcendental roundings are fixed (fp64 sum of squares
+ * rounded once, rsqrt = 1/sqrtf, exp in fp64 rounded to fp32) so the output is
+ * reproducible bit for bit.
+ * ------------------------------------------------------------------------- */
+
+/* (add +) RMSNorm -> FP8: h = x (+ residual); normed = h * rsqrt(mean(h^2) + eps)
+ * * weight, rounded to dtype, then per-token quant.  With residual != NULL,
+ * hidden_out receives h in dtype.  Replaces triton_rms_norm_fp8_per_token /
+ * triton_add_rms_norm_fp8_per_token (src/torchinferno/kernels/triton_ops.py:
+ * 2127-2182, 2226-2297). */
+int ti_fp8_rmsnorm_quant_per_token(const void* x, const void* residual, const void* weight, int dtype,
+                                   int rows, int n, float eps, void* hidden_out, uint8_t* xq, float* xs,
+                                   hipStream_t stream);
+
+/* SwiGLU -> FP8: act = g / (1 + exp(-g)) * u rounded to dtype, then per-token
+ * quant; gate / up rows are row_stride elements apart (split views allowed).
+ * Replaces triton_swiglu_fp8_per_token (triton_ops.py:2185-2223, 2300-2333). */
+int ti_fp8_swiglu_quant_per_token(const void* gate, long gate_row_stride, const void* up,
+                                  long up_row_stride, int dtype, int rows, int n, uint8_t* xq, float* xs,
+                                  hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
  * FP8 W8A8 GEMMs: out[M,N] = a[M,K] . b[N,K]^T (both e4m3, K-contiguous, the
  * "b = weight.t(), column-major" layout of torch._scaled_mm), fp32
  * accumulation, out bf16 or fp16.  Requires K % 128 == 0; M, N arbitrary.

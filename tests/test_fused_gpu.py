@@ -1,0 +1,131 @@
+"""Fused (add +) RMSNorm / SwiGLU -> per-token FP8 producers on the GPU: codes,
+scales and the summed hidden state equal oracle/fused.py bit for bit, and the
+reference test's restore tolerances hold (tests/test_conversion_and_kernels.py:
+390-435 of the reference, same shapes and seed)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import fused as ofu
+from oracle.numerics import e4m3_decode
+
+pytestmark = pytest.mark.gpu
+
+_ACT = {torch.bfloat16: "bf16", torch.float16: "fp16"}
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def _codes(q):
+    return q.reshape(-1, q.size(-1)).view(torch.uint8).cpu().numpy()
+
+
+def test_reference_restore_tolerances(dev):
+    from torchinferno_amd.kernels import fused
+    torch.manual_seed(17)
+    x = torch.randn((7, 64), device=dev, dtype=torch.bfloat16)
+    residual = torch.randn_like(x)
+    weight = torch.randn((64,), device=dev, dtype=torch.bfloat16)
+    eps = 1e-5
+    q, s = fused.triton_rms_norm_fp8_per_token(x, weight, eps)
+    exp = x.float() * torch.rsqrt(x.float().square().mean(-1, keepdim=True) + eps) * weight.float()
+    torch.testing.assert_close(q.float() * s, exp, atol=1.2e-1, rtol=1.3e-1)
+    h, q2, s2 = fused.triton_add_rms_norm_fp8_per_token(x, residual, weight, eps)
+    hs = x.float() + residual.float()
+    exp2 = hs * torch.rsqrt(hs.square().mean(-1, keepdim=True) + eps) * weight.float()
+    torch.testing.assert_close(h, x + residual, atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(q2.float() * s2, exp2, atol=1.2e-1, rtol=1.3e-1)
+    gate, up = torch.randn((7, 128), device=dev, dtype=torch.bfloat16).split(64, dim=-1)
+    q3, s3 = fused.triton_swiglu_fp8_per_token(gate, up)
+    exp3 = torch.nn.functional.silu(gate.float()) * up.float()
+    torch.testing.assert_close(q3.float() * s3, exp3, atol=1.2e-1, rtol=1.3e-1)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,n", [(1, 4096), (5, 8), (33, 2056), (3, 16384), (130, 8192)])
+def test_rmsnorm_bit_exact(dev, dt, rows, n):
+    from torchinferno_amd.kernels import fused
+    g = torch.Generator(device=dev).manual_seed(rows * 7 + n)
+    x = (torch.randn((rows, n), generator=g, device=dev) * 3).to(dt)
+    r = torch.randn((rows, n), generator=g, device=dev).to(dt)
+    w = (torch.rand((n,), generator=g, device=dev) + 0.5).to(dt)
+    x[0, : n // 2] = 0  # a half-zero row
+    eps = 1e-6
+    q, s = fused.rms_norm_fp8_per_token(x, w, eps)
+    oq, os_ = ofu.rms_norm_fp8_per_token(_np(x), _np(w), eps, _ACT[dt])
+    assert np.array_equal(_codes(q), oq) and np.array_equal(s.cpu().numpy(), os_)
+    h, q2, s2 = fused.add_rms_norm_fp8_per_token(x, r, w, eps)
+    oh, oq2, os2 = ofu.add_rms_norm_fp8_per_token(_np(x), _np(r), _np(w), eps, _ACT[dt])
+    assert h.dtype == dt and np.array_equal(_np(h), oh)
+    assert np.array_equal(_codes(q2), oq2) and np.array_equal(s2.cpu().numpy(), os2)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,n", [(1, 14336), (4, 8), (17, 1032), (64, 4096)])
+def test_swiglu_bit_exact_on_split_views(dev, dt, rows, n):
+    from torchinferno_amd.kernels import fused
+    g = torch.Generator(device=dev).manual_seed(rows + n)
+    gu = (torch.randn((rows, 1, 2 * n), generator=g, device=dev) * 4).to(dt)
+    gate, up = gu.split((n, n), dim=-1)  # strided rows, as the Llama3 MLP hands them over
+    q, s = fused.swiglu_fp8_per_token(gate, up)
+    assert q.shape == gate.shape and s.shape == (rows, 1)
+    oq, os_ = ofu.swiglu_fp8_per_token(_np(gate).reshape(rows, n), _np(up).reshape(rows, n), _ACT[dt])
+    assert np.array_equal(_codes(q), oq) and np.array_equal(s.cpu().numpy(), os_)
+
+
+def test_zero_rows_and_errors(dev):
+    from torchinferno_amd.kernels import fused
+    x = torch.zeros((2, 64), device=dev, dtype=torch.bfloat16)
+    w = torch.ones((64,), device=dev, dtype=torch.bfloat16)
+    q, s = fused.rms_norm_fp8_per_token(x, w, 1e-6)  # all-zero rows: scale floor, zero codes
+    assert torch.all(s == 1e-10) and not _codes(q).any()
+    e = torch.empty((0, 64), device=dev, dtype=torch.bfloat16)
+    q, s = fused.rms_norm_fp8_per_token(e, w, 1e-6)
+    assert q.shape == (0, 64) and s.shape == (0, 1)
+    with pytest.raises(ValueError):
+        fused.rms_norm_fp8_per_token(x.float(), w, 1e-6)
+    with pytest.raises(ValueError):
+        fused.rms_norm_fp8_per_token(x, w[:32], 1e-6)
+    with pytest.raises(ValueError):
+        fused.add_rms_norm_fp8_per_token(x, x[:1], w, 1e-6)
+    with pytest.raises(ValueError):
+        fused.swiglu_fp8_per_token(x, x.half())
+    with pytest.raises(ValueError):
+        fused.swiglu_fp8_per_token(x.t(), x.t())
+
+
+def test_feeds_per_token_linear(dev):
+    """SwiGLU -> FP8 -> per-token GEMM equals the GEMM on the separately quantized
+    activation (the Llama3 down-projection chain, tensor_parallel.py:3183-3200)."""
+    from torchinferno_amd.kernels import fp8 as tf8
+    from torchinferno_amd.kernels import fused
+    g = torch.Generator(device=dev).manual_seed(9)
+    gu = torch.randn((8, 2048), generator=g, device=dev).to(torch.bfloat16)
+    gate, up = gu.split(1024, dim=-1)
+    wq, ws = tf8.quantize_weight_fp8_per_channel(
+        (torch.randn((512, 1024), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+    q, s = fused.swiglu_fp8_per_token(gate, up)
+    act = (torch.nn.functional.silu(gate.float()) * up.float()).to(torch.bfloat16)
+    q2, s2 = tf8.quantize_activation_fp8_per_token(act)
+    y1 = tf8.fp8_per_token_linear_quantized(q, s, wq, ws, out_dtype=torch.bfloat16)
+    y2 = tf8.fp8_per_token_linear_quantized(q2, s2, wq, ws, out_dtype=torch.bfloat16)
+    torch.testing.assert_close(y1.float(), y2.float(), atol=2e-2, rtol=5e-2)
+
+
+def test_ops_and_patch(dev):
+    import types
+    from torchinferno_amd import hooks, ops  # noqa: F401
+    from torchinferno_amd.kernels import fused
+    x = torch.randn((4, 256), device=dev, dtype=torch.bfloat16)
+    w = torch.rand((256,), device=dev, dtype=torch.bfloat16)
+    torch.library.opcheck(torch.ops.torchinferno_amd.add_rms_norm_fp8_per_token, (x, x, w, 1e-6),
+                          test_utils=("test_faketensor",))
+    torch.library.opcheck(torch.ops.torchinferno_amd.swiglu_fp8_per_token, (x, x),
+                          test_utils=("test_faketensor",))
+    mod = types.ModuleType("fake_triton_ops")
+    undo = hooks.patch_fused_producers(mod)
+    assert mod.triton_swiglu_fp8_per_token is fused.swiglu_fp8_per_token
+    undo()
+    assert not hasattr(mod, "triton_swiglu_fp8_per_token")

@@ -172,7 +172,7 @@ def test_decode_kernel_plans(dev, monkeypatch, plan, m):
 
 # Tall tiles (64 / 128 staged rows): each instantiated (nt, wk, ring) with and
 # without split-K, ragged M, both activation dtypes.
-_TALL_PLANS = ["2:2:2:1", "4:1:2:1", "4:1:3:2", "2:1:3:1", "2:1:4:3"]
+_TALL_PLANS = ["2:2:2:1", "4:1:2:1", "4:1:3:2", "2:1:3:1", "2:1:4:3", "2:1:2:1", "2:1:2:2"]
 
 
 @pytest.mark.parametrize("plan", _TALL_PLANS)

@@ -1,0 +1,54 @@
+"""Pins oracle/fused.py (CPU): the reference test's restore tolerances against
+plain torch float math (tests/test_conversion_and_kernels.py:390-435, seed 17),
+"fused == norm then per-token quant", and closed forms of the norm."""
+import numpy as np
+import torch
+
+from oracle import fused as ofu
+from oracle.fp8 import quantize_activation_per_token
+from oracle.numerics import e4m3_decode, round_to
+
+F32 = np.float32
+
+
+def test_reference_restore_tolerances():
+    torch.manual_seed(17)
+    x = torch.randn((7, 64), dtype=torch.bfloat16)
+    residual = torch.randn_like(x)
+    weight = torch.randn((64,), dtype=torch.bfloat16)
+    eps = 1e-5
+    xn, rn, wn = x.float().numpy(), residual.float().numpy(), weight.float().numpy()
+    expected = (x.float() * torch.rsqrt(x.float().square().mean(-1, keepdim=True) + eps) * weight.float()).numpy()
+    q, s = ofu.rms_norm_fp8_per_token(xn, wn, eps, "bf16")
+    np.testing.assert_allclose(e4m3_decode(q) * s, expected, atol=1.2e-1, rtol=1.3e-1)
+    h = (x.float() + residual.float())
+    expected2 = (h * torch.rsqrt(h.square().mean(-1, keepdim=True) + eps) * weight.float()).numpy()
+    hid, q2, s2 = ofu.add_rms_norm_fp8_per_token(xn, rn, wn, eps, "bf16")
+    np.testing.assert_allclose(hid, (x + residual).float().numpy(), atol=2e-2, rtol=2e-2)
+    np.testing.assert_allclose(e4m3_decode(q2) * s2, expected2, atol=1.2e-1, rtol=1.3e-1)
+    gate, up = torch.randn((7, 128), dtype=torch.bfloat16).split(64, dim=-1)
+    exp3 = (torch.nn.functional.silu(gate.float()) * up.float()).numpy()
+    q3, s3 = ofu.swiglu_fp8_per_token(gate.float().numpy(), up.float().numpy(), "bf16")
+    np.testing.assert_allclose(e4m3_decode(q3) * s3, exp3, atol=1.2e-1, rtol=1.3e-1)
+
+
+def test_fused_is_norm_then_quant():
+    rng = np.random.default_rng(0)
+    x = round_to(rng.standard_normal((5, 96)).astype(F32), "fp16")
+    w = round_to(rng.standard_normal(96).astype(F32), "fp16")
+    q, s = ofu.rms_norm_fp8_per_token(x, w, 1e-6, "fp16")
+    q2, s2 = quantize_activation_per_token(round_to(ofu._rms(x, w, 1e-6), "fp16"))
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+
+
+def test_rms_closed_forms():
+    # constant rows: rms = |c|, so normed = sign(c) * w (up to eps)
+    x = np.full((2, 8), 3.0, F32)
+    x[1] = -0.5
+    w = np.arange(1, 9, dtype=F32)
+    out = ofu._rms(x, w, 0.0)
+    np.testing.assert_allclose(out[0], w, rtol=1e-6)
+    np.testing.assert_allclose(out[1], -w, rtol=1e-6)
+    # silu(0) * u = 0; silu(large) ~ g
+    a = ofu.swiglu_activation(np.array([[0.0, 30.0]], F32), np.array([[5.0, 2.0]], F32), "fp32")
+    assert a[0, 0] == 0.0 and abs(a[0, 1] - 60.0) < 1e-3

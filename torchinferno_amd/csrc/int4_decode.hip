@@ -266,7 +266,8 @@ void launch_nt(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
 }
 
 // Tall tiles (64 / 128 staged rows) instantiate a curated set of
-// (nt, wk, ring) configurations; make_decode_plan only produces these.
+// (nt, wk, ring) configurations -- (2,2,2), (4,1,2|3), (2,1,2|3|4); the plan
+// only produces these.
 template <int DT, int MR>
 void launch_tall(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
   if (p.wk == 2) launch_split<DT, MR, 2, 2, 2>(p, x, stream);
@@ -275,6 +276,7 @@ void launch_tall(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
     else launch_split<DT, MR, 4, 1, 3>(p, x, stream);
   } else {
     if (p.ring == 4) launch_split<DT, MR, 2, 1, 4>(p, x, stream);
+    else if (p.ring == 2) launch_split<DT, MR, 2, 1, 2>(p, x, stream);
     else launch_split<DT, MR, 2, 1, 3>(p, x, stream);
   }
 }
@@ -338,13 +340,13 @@ DecodePlan make_decode_plan(int M, int N, int K) {
     }
   }
   if (tall) {
-    // The instantiated tall configurations: (2,2,2), (4,1,2|3), (2,1,3|4); a
+    // The instantiated tall configurations: (2,2,2), (4,1,2|3), (2,1,2|3|4); a
     // workgroup covers 256 / 128 / 64 columns, which must divide N.
     if (p.wk == 1 && p.nt >= 4 && N % 256) p.nt = 2;
     if (p.wk == 1 && p.nt < 4 && N % 128) p.wk = 2;
     if (p.wk != 1) { p.wk = 2; p.nt = 2; p.ring = 2; }
     else if (p.nt >= 4) { p.nt = 4; p.ring = p.ring <= 2 ? 2 : 3; }
-    else { p.nt = 2; p.ring = p.ring >= 4 ? 4 : 3; }
+    else { p.nt = 2; p.ring = p.ring >= 4 ? 4 : (p.ring <= 2 ? 2 : 3); }
   } else {
     if (p.nt != 1 && p.nt != 2 && p.nt != 4) p.nt = 2;
     if (p.wk != 1 && p.wk != 2 && p.wk != 4) p.wk = 1;
@@ -362,7 +364,6 @@ DecodePlan make_decode_plan(int M, int N, int K) {
   auto fits = [&](int r) { return r * stage_bytes(p.mr, p.nt, p.wk) + sbytes <= kDecodeLdsMax; };
   if (tall) {
     while (p.ring > 2 && !fits(p.ring)) p.ring = p.ring == 4 ? 3 : 2;
-    if (p.ring == 2 && p.nt == 2 && p.wk == 1) p.ring = 3;  // (2,1,2) is not instantiated
   } else {
     while (p.ring > 3 && !fits(p.ring)) p.ring = p.ring == 6 ? 4 : 3;
   }
@@ -377,7 +378,7 @@ bool decode_plan_valid(const DecodePlan& p, int N) {
   if (N % (kWaves / p.wk * p.nt * 16) || p.nblocks * (kWaves / p.wk * p.nt * 16) != N) return false;
   if (p.mr >= 64)
     return (p.nt == 2 && p.wk == 2 && p.ring == 2) || (p.nt == 4 && p.wk == 1 && (p.ring == 2 || p.ring == 3)) ||
-           (p.nt == 2 && p.wk == 1 && (p.ring == 3 || p.ring == 4));
+           (p.nt == 2 && p.wk == 1 && (p.ring >= 2 && p.ring <= 4));
   return (p.nt == 1 || p.nt == 2 || p.nt == 4) && (p.wk == 1 || p.wk == 2 || p.wk == 4) &&
          (p.ring == 3 || p.ring == 4 || p.ring == 6) && (p.mr == 4 || p.mr == 16 || p.mr == 32);
 }

@@ -409,7 +409,8 @@ static Plan make_plan(int M, int N, int K) {
   }
   if (p.nt != 1 && p.nt != 2 && p.nt != 4) p.nt = 4;
   if (p.waves != 4 && p.waves != 8) p.waves = 4;
-  if (p.depth != 2 && p.depth != 4) p.depth = 2;
+  if (p.depth != 2 && p.depth != 4 && p.depth != 8) p.depth = 2;
+  if (p.depth == 8 && (p.mt != 1 || p.nt > 2)) p.depth = 4;  // depth 8: single-row-tile, narrow plans only
   if (N % (p.nt * 16)) p.nt = 1;
   p.nblocks = N / (p.nt * 16);
   p.splits = max(1, min(p.splits, NG));
@@ -633,7 +634,13 @@ static void launch_al(const Plan& p, const LaunchArgs& x, hipStream_t stream) {
 
 template <int DT, int MT, int NT, int W>
 static void launch_d(const Plan& p, const LaunchArgs& x, hipStream_t stream) {
-  if (p.depth == 4) launch_al<DT, MT, NT, W, 4>(p, x, stream);
+  if constexpr (MT == 1 && NT <= 2) {
+    if (p.depth == 8) {
+      launch_al<DT, MT, NT, W, 8>(p, x, stream);
+      return;
+    }
+  }
+  if (p.depth >= 4) launch_al<DT, MT, NT, W, 4>(p, x, stream);
   else launch_al<DT, MT, NT, W, 2>(p, x, stream);
 }
 

@@ -253,6 +253,31 @@ def patch_llama3_layer_class(cls: type) -> Callable[[], None]:
     return undo
 
 
+_FUSED_NAMES = ("triton_rms_norm_fp8_per_token", "triton_add_rms_norm_fp8_per_token",
+                "triton_swiglu_fp8_per_token")
+
+
+def patch_fused_producers(module: types.ModuleType) -> Callable[[], None]:
+    """Point the fused RMSNorm / add+RMSNorm / SwiGLU -> per-token FP8 producers of
+    ``module`` (the reference's ``torchinferno.kernels.triton_ops``, which the
+    Llama3 layer imports from at call time, tensor_parallel.py:3073-3187) at this
+    package's kernels.  Returns undo."""
+    from .kernels import fused
+
+    saved = {n: getattr(module, n, None) for n in _FUSED_NAMES}
+    for n in _FUSED_NAMES:
+        setattr(module, n, getattr(fused, n))
+
+    def undo() -> None:
+        for n, orig in saved.items():
+            if orig is None:
+                delattr(module, n)
+            else:
+                setattr(module, n, orig)
+
+    return undo
+
+
 # --------------------------------------------------------------------------- DeepSeek-V4
 
 

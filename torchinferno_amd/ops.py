@@ -18,14 +18,18 @@ Ops (each a thin wrapper over ``torchinferno_amd.kernels.*`` and libti_quant.so)
   (deepseek_v4_tilelang.py:147-223);
 * ``moe_route_topk(logits, k, renormalize, route_scale) -> (Tensor, Tensor)`` and
   ``fused_fp8_moe(hidden, topk_weights, topk_ids, w13, w13_scale, w2, w2_scale,
-  clamp_limit) -> Tensor`` -- the routed-expert slot (deepseek_v4_marlin.py:311).
+  clamp_limit) -> Tensor`` -- the routed-expert slot (deepseek_v4_marlin.py:311);
+* ``rms_norm_fp8_per_token(x, weight, eps) -> (q, scale)``,
+  ``add_rms_norm_fp8_per_token(x, residual, weight, eps) -> (hidden, q, scale)``,
+  ``swiglu_fp8_per_token(gate, up) -> (q, scale)`` -- the fused producers of the
+  per-token FP8 linear (triton_ops.py:2239-2333).
 """
 from __future__ import annotations
 
 import torch
 from torch import Tensor
 
-from .kernels import block_fp8, fp8, int4, moe
+from .kernels import block_fp8, fp8, fused, int4, moe
 
 _NS = "torchinferno_amd"
 
@@ -132,3 +136,45 @@ def fused_fp8_moe(hidden: Tensor, topk_weights: Tensor, topk_ids: Tensor, w13: T
 @fused_fp8_moe.register_fake
 def _fused_fp8_moe_fake(hidden, topk_weights, topk_ids, w13, w13_scale, w2, w2_scale, clamp_limit):
     return torch.empty_like(hidden)
+
+
+# --------------------------------------------------------------------------- fused producers
+
+
+@torch.library.custom_op(f"{_NS}::rms_norm_fp8_per_token", mutates_args=())
+def rms_norm_fp8_per_token(x: Tensor, weight: Tensor, eps: float) -> tuple[Tensor, Tensor]:
+    q, s = fused.rms_norm_fp8_per_token(x, weight, eps)
+    return q, s
+
+
+@rms_norm_fp8_per_token.register_fake
+def _rms_norm_fp8_fake(x, weight, eps):
+    rows = x.numel() // x.size(-1)
+    return torch.empty_like(x, dtype=torch.float8_e4m3fn), x.new_empty((rows, 1), dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{_NS}::add_rms_norm_fp8_per_token", mutates_args=())
+def add_rms_norm_fp8_per_token(x: Tensor, residual: Tensor, weight: Tensor,
+                               eps: float) -> tuple[Tensor, Tensor, Tensor]:
+    h, q, s = fused.add_rms_norm_fp8_per_token(x, residual, weight, eps)
+    return h, q, s
+
+
+@add_rms_norm_fp8_per_token.register_fake
+def _add_rms_norm_fp8_fake(x, residual, weight, eps):
+    rows = x.numel() // x.size(-1)
+    return (torch.empty_like(x), torch.empty_like(x, dtype=torch.float8_e4m3fn),
+            x.new_empty((rows, 1), dtype=torch.float32))
+
+
+@torch.library.custom_op(f"{_NS}::swiglu_fp8_per_token", mutates_args=())
+def swiglu_fp8_per_token(gate: Tensor, up: Tensor) -> tuple[Tensor, Tensor]:
+    q, s = fused.swiglu_fp8_per_token(gate, up)
+    return q, s
+
+
+@swiglu_fp8_per_token.register_fake
+def _swiglu_fp8_fake(gate, up):
+    rows = gate.numel() // gate.size(-1)
+    return (gate.new_empty(gate.shape, dtype=torch.float8_e4m3fn),
+            gate.new_empty((rows, 1), dtype=torch.float32))
