@@ -13,7 +13,8 @@ HBM GB/s over the packed-weight + scale bytes of a step (the config's unit).
 algorithmic bytes (or flops) over its average duration, measured with HIP
 events on the stream the kernel runs on.  ``points`` lists every BASELINE
 config measured the same way: config 0 (int4 fp16), config 2 (FP8 per-token x
-per-channel, Llama-3-70B), config 3 (DeepSeek 128x128 block FP8) and config 4
+per-channel, Llama-3-70B, plus its fused add+RMSNorm / SwiGLU -> FP8
+activation producers), config 3 (DeepSeek 128x128 block FP8) and config 4
 (routed FP8 MoE, 256 experts, top-8, router included).  ``cpu_baseline`` times
 the CPU oracle (dequantize-then-matmul, oracle/int4.py) on one gate_up M=32 GEMM.
 
@@ -251,6 +252,50 @@ def fp8_points(dev, stream):
     return recs
 
 
+# --------------------------------------------------------------------------- fused producers
+
+
+def fused_points(dev, stream):
+    """Config 2's activation producers: add+RMSNorm -> FP8 over the hidden size
+    (8192) and SwiGLU -> FP8 over the intermediate size (28672, gate/up as split
+    views of one [M, 2I] tensor).  HBM-bound: algorithmic bytes are the reads of
+    x, residual and the norm weight plus the writes of hidden, codes and scales
+    (2+2+2+1 bytes per element), resp. gate + up reads and code writes (2+2+1)."""
+    import torch
+    from torchinferno_amd import _lib
+    L = _lib.lib()
+    recs = []
+    hsz, isz = 8192, 28672
+    for m in (1, 64, 4096):
+        x = torch.randn((m, hsz), device=dev).to(torch.bfloat16)
+        r = torch.randn_like(x)
+        w = torch.rand((hsz,), device=dev).to(torch.bfloat16)
+        hid = torch.empty_like(x)
+        q = torch.empty((m, hsz), dtype=torch.uint8, device=dev)
+        sc = torch.empty((m,), dtype=torch.float32, device=dev)
+
+        def norm(st, x=x, r=r, w=w, hid=hid, q=q, sc=sc, m=m):
+            _check("rmsnorm", L.ti_fp8_rmsnorm_quant_per_token(x.data_ptr(), r.data_ptr(), w.data_ptr(), 2, m, hsz,
+                                                               1e-5, hid.data_ptr(), q.data_ptr(), sc.data_ptr(), st))
+
+        gu = torch.randn((m, 2 * isz), device=dev).to(torch.bfloat16)
+        q2 = torch.empty((m, isz), dtype=torch.uint8, device=dev)
+        sc2 = torch.empty((m,), dtype=torch.float32, device=dev)
+
+        def swiglu(st, gu=gu, q2=q2, sc2=sc2, m=m):
+            _check("swiglu", L.ti_fp8_swiglu_quant_per_token(gu.data_ptr(), 2 * isz, gu.data_ptr() + isz * 2,
+                                                             2 * isz, 2, m, isz, q2.data_ptr(), sc2.data_ptr(), st))
+
+        for label, fn, algo in ((f"config2 add_rmsnorm_fp8 M={m} H={hsz}", norm, m * hsz * 7 + hsz * 2 + m * 4),
+                                (f"config2 swiglu_fp8 M={m} I={isz}", swiglu, m * isz * 5 + m * 4)):
+            reps = 20 if m >= 4096 else 200
+            timed_burst([fn], 5, stream)
+            t = timed_burst([fn], reps, stream) / reps * 1e-3
+            recs.append(point_record(label, t, algo, 0, "hbm", FP8_PEAK_TFLOPS))
+            log(recs[-1])
+    return recs
+
+
 # --------------------------------------------------------------------------- MoE
 
 
@@ -343,6 +388,7 @@ def main():
     extra_points = []
     if args.only in (None, "fp8"):
         extra_points += fp8_points(dev, stream)
+        extra_points += fused_points(dev, stream)
     if args.only in (None, "moe"):
         extra_points += moe_points(dev, stream)
     if args.only in ("fp8", "moe"):

@@ -44,7 +44,7 @@ def test_reference_restore_tolerances(dev):
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("rows,n", [(1, 4096), (5, 8), (33, 2056), (3, 16384), (130, 8192)])
+@pytest.mark.parametrize("rows,n", [(1, 4096), (5, 8), (33, 2056), (3, 16384), (130, 8192), (2, 65536), (4, 24576)])
 def test_rmsnorm_bit_exact(dev, dt, rows, n):
     from torchinferno_amd.kernels import fused
     g = torch.Generator(device=dev).manual_seed(rows * 7 + n)
@@ -63,7 +63,7 @@ def test_rmsnorm_bit_exact(dev, dt, rows, n):
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("rows,n", [(1, 14336), (4, 8), (17, 1032), (64, 4096)])
+@pytest.mark.parametrize("rows,n", [(1, 14336), (4, 8), (17, 1032), (64, 4096), (2, 40000), (3, 28672)])
 def test_swiglu_bit_exact_on_split_views(dev, dt, rows, n):
     from torchinferno_amd.kernels import fused
     g = torch.Generator(device=dev).manual_seed(rows + n)
@@ -94,6 +94,9 @@ def test_zero_rows_and_errors(dev):
         fused.swiglu_fp8_per_token(x, x.half())
     with pytest.raises(ValueError):
         fused.swiglu_fp8_per_token(x.t(), x.t())
+    wide = torch.zeros((1, 65544), device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        fused.swiglu_fp8_per_token(wide, wide)
 
 
 def test_feeds_per_token_linear(dev):

@@ -52,3 +52,22 @@ def test_rms_closed_forms():
     # silu(0) * u = 0; silu(large) ~ g
     a = ofu.swiglu_activation(np.array([[0.0, 30.0]], F32), np.array([[5.0, 2.0]], F32), "fp32")
     assert a[0, 0] == 0.0 and abs(a[0, 1] - 60.0) < 1e-3
+
+
+def test_exp_rounding_is_implementation_independent():
+    """The SwiGLU producers evaluate exp(-g) in fp64 and round to fp32.  For every
+    finite bf16 and fp16 g, exp(-g) lies at least 2^-51 (relative) from an fp32
+    rounding midpoint, so any fp64 exp accurate to 1 ulp (2^-52) -- numpy's, the
+    GPU math library's -- rounds to the same fp32 value: the oracle's choice is
+    reproducible on the device for all inputs."""
+    with np.errstate(over="ignore"):
+        for vals in ((np.arange(65536, dtype=np.uint32) << 16).view(F32),
+                     np.arange(65536, dtype=np.uint16).view(np.float16).astype(F32)):
+            g = vals[np.isfinite(vals)].astype(np.float64)
+            e = np.exp(-g)
+            e = e[(e > 0) & (e < 3.0e38)]
+            f = e.astype(F32)
+            f64 = f.astype(np.float64)
+            nxt = np.where(e >= f64, np.nextafter(f, F32(np.inf)), np.nextafter(f, F32(0))).astype(np.float64)
+            mid = (f64 + nxt) / 2
+            assert (np.abs(e - mid) / e).min() >= 2.0 ** -51

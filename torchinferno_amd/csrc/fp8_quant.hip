@@ -15,6 +15,8 @@
 // All arithmetic is fp32 with IEEE division (no reciprocal approximation), and
 // the cast is round-to-nearest-even, so codes and scales are bit-identical to
 // the same formulas evaluated by torch on the host.
+#include <type_traits>
+
 #include "fp8_common.h"
 
 namespace ti {
@@ -125,22 +127,31 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(const uint16_t* __res
 }
 
 
-// Block-wide sums / maxima over 256 threads (4 waves).
-__device__ __forceinline__ double block_sum_f64(double v, double* red) {
+// ---- fused producers: one 1024-thread workgroup per row, the row held in
+// registers (V vectors of 8 per thread, n <= 8192 * V), so HBM is read once and
+// each element's arithmetic is done once.
+constexpr int kRowThreads = 1024;
+constexpr int kRowWaves = kRowThreads / 64;
+
+__device__ __forceinline__ double row_sum_f64(double v, double* red) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  return (red[0] + red[1]) + (red[2] + red[3]);
+  double t = 0.0;
+#pragma unroll
+  for (int i = 0; i < kRowWaves; ++i) t += red[i];
+  return t;
 }
 
-__device__ __forceinline__ float block_max_f32(float v, float* red) {
+__device__ __forceinline__ float row_max_f32(float v, float* red) {
   v = wave_max(v);
-  __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRowWaves; ++i) t = fmaxf(t, red[i]);
+  return t;
 }
 
 // fp32 -> activation dtype -> fp32.  The empty asm pins f as an fp32 register
@@ -161,101 +172,109 @@ __device__ __forceinline__ uint4 pack_act8(const float (&f)[8]) {
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// (add +) RMSNorm -> per-token e4m3, one workgroup per row; n % 8 == 0.
-// Sum of squares in fp64 rounded once to fp32; rsqrt = 1/sqrtf (IEEE); the
-// normalized row is rounded to the activation dtype before the quant.
-template <int DT, bool ADD>
-__global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const uint16_t* __restrict__ x,
-                                                            const uint16_t* __restrict__ res,
-                                                            const uint16_t* __restrict__ w, int n, float eps,
-                                                            uint16_t* __restrict__ hidden, uint8_t* __restrict__ q,
-                                                            float* __restrict__ s) {
-  __shared__ double redd[4];
-  __shared__ float redf[4];
-  const long row = blockIdx.x;
-  const uint16_t* xr = x + row * n;
-  const uint16_t* rr = ADD ? res + row * n : nullptr;
-  auto load_h = [&](int i, float (&h)[8]) {
-    load8<DT>(xr + i, h);
-    if constexpr (ADD) {
-      float r[8];
-      load8<DT>(rr + i, r);
+// Quantize the row held in v with scale max(amax / 448, 1e-10) and store it.
+template <int V>
+__device__ __forceinline__ void row_quant_store(float (&v)[V][8], float amax, int n, uint8_t* __restrict__ qr,
+                                                float* __restrict__ s_out) {
+  const float sc = fmaxf(amax / kE4M3Max, 1e-10f);
+  if (threadIdx.x == 0) *s_out = sc;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) h[e] = h[e] + r[e];
+  for (int j = 0; j < V; ++j) {
+    const int i = (j * kRowThreads + threadIdx.x) * 8;
+    if (i < n) {
+      uint32_t c[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) c[e] = e4m3_encode(v[j][e] / sc);
+      *(uint2*)(qr + i) = pack8(c);
     }
-  };
-  double ss = 0.0;
-  for (int i = threadIdx.x * 8; i < n; i += 256 * 8) {
-    float h[8];
-    load_h(i, h);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss += (double)h[e] * (double)h[e];
-    if constexpr (ADD) *(uint4*)(hidden + row * n + i) = pack_act8<DT>(h);
   }
-  ss = block_sum_f64(ss, redd);
+}
+
+// (add +) RMSNorm -> per-token e4m3; n % 8 == 0, n <= 8192 * V.  Sum of
+// squares in fp64 rounded once to fp32; rsqrt = 1/sqrtf (IEEE); the normalized
+// row is rounded to the activation dtype before the quant.
+template <int DT, int V, bool ADD>
+__global__ __launch_bounds__(kRowThreads) void rmsnorm_quant_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ res, const uint16_t* __restrict__ w, int n,
+    float eps, uint16_t* __restrict__ hidden, uint8_t* __restrict__ q, float* __restrict__ s) {
+  __shared__ double redd[kRowWaves];
+  __shared__ float redf[kRowWaves];
+  const long row = blockIdx.x;
+  float h[V][8];
+  double ss = 0.0;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int i = (j * kRowThreads + threadIdx.x) * 8;
+    if (i < n) {
+      load8<DT>(x + row * n + i, h[j]);
+      if constexpr (ADD) {
+        float r[8];
+        load8<DT>(res + row * n + i, r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[j][e] = h[j][e] + r[e];
+        *(uint4*)(hidden + row * n + i) = pack_act8<DT>(h[j]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += (double)h[j][e] * (double)h[j][e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[j][e] = 0.f;
+    }
+  }
+  ss = row_sum_f64(ss, redd);
   const float var = (float)ss / (float)n;
   const float rs = 1.0f / sqrtf(var + eps);
   float amax = 0.f;
-  for (int i = threadIdx.x * 8; i < n; i += 256 * 8) {
-    float h[8], wt[8];
-    load_h(i, h);
-    load8<DT>(w + i, wt);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(round_act<DT>(h[e] * rs * wt[e])));
-  }
-  amax = block_max_f32(amax, redf);
-  const float sc = fmaxf(amax / kE4M3Max, 1e-10f);
-  if (threadIdx.x == 0) s[row] = sc;
-  for (int i = threadIdx.x * 8; i < n; i += 256 * 8) {
-    float h[8], wt[8];
-    load_h(i, h);
-    load8<DT>(w + i, wt);
-    uint32_t c[8];
+  for (int j = 0; j < V; ++j) {
+    const int i = (j * kRowThreads + threadIdx.x) * 8;
+    if (i < n) {
+      float wt[8];
+      load8<DT>(w + i, wt);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) c[e] = e4m3_encode(round_act<DT>(h[e] * rs * wt[e]) / sc);
-    *(uint2*)(q + row * n + i) = pack8(c);
+      for (int e = 0; e < 8; ++e) {
+        h[j][e] = round_act<DT>(h[j][e] * rs * wt[e]);
+        amax = fmaxf(amax, fabsf(h[j][e]));
+      }
+    }
   }
+  amax = row_max_f32(amax, redf);
+  row_quant_store<V>(h, amax, n, q + row * n, s + row);
 }
 
 // SwiGLU -> per-token e4m3: act = g / (1 + exp(-g)) * u (exp in fp64, rounded
 // to fp32), rounded to the activation dtype.  Rows of gate/up are strided.
-template <int DT>
-__global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __restrict__ gate, long gstride,
-                                                           const uint16_t* __restrict__ up, long ustride, int n,
-                                                           uint8_t* __restrict__ q, float* __restrict__ s) {
-  __shared__ float redf[4];
+template <int DT, int V>
+__global__ __launch_bounds__(kRowThreads) void swiglu_quant_kernel(const uint16_t* __restrict__ gate, long gstride,
+                                                                   const uint16_t* __restrict__ up, long ustride,
+                                                                   int n, uint8_t* __restrict__ q,
+                                                                   float* __restrict__ s) {
+  __shared__ float redf[kRowWaves];
   const long row = blockIdx.x;
-  const uint16_t* gr = gate + row * gstride;
-  const uint16_t* ur = up + row * ustride;
-  auto act8 = [&](int i, float (&a)[8]) {
-    float g[8], u[8];
-    load8<DT>(gr + i, g);
-    load8<DT>(ur + i, u);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float ex = (float)exp(-(double)g[e]);
-      a[e] = round_act<DT>(g[e] / (1.0f + ex) * u[e]);
-    }
-  };
+  float a[V][8];
   float amax = 0.f;
-  for (int i = threadIdx.x * 8; i < n; i += 256 * 8) {
-    float a[8];
-    act8(i, a);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(a[e]));
-  }
-  amax = block_max_f32(amax, redf);
-  const float sc = fmaxf(amax / kE4M3Max, 1e-10f);
-  if (threadIdx.x == 0) s[row] = sc;
-  for (int i = threadIdx.x * 8; i < n; i += 256 * 8) {
-    float a[8];
-    act8(i, a);
-    uint32_t c[8];
+  for (int j = 0; j < V; ++j) {
+    const int i = (j * kRowThreads + threadIdx.x) * 8;
+    if (i < n) {
+      float g[8], u[8];
+      load8<DT>(gate + row * gstride + i, g);
+      load8<DT>(up + row * ustride + i, u);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) c[e] = e4m3_encode(a[e] / sc);
-    *(uint2*)(q + row * n + i) = pack8(c);
+      for (int e = 0; e < 8; ++e) {
+const float ex = (float)exp(-(double)g[e]);
+        a[j][e] = round_act<DT>(g[e] / (1.0f + ex) * u[e]);
+        amax = fmaxf(amax, fabsf(a[j][e]));
+      }
+    }
   }
+  amax = row_max_f32(amax, redf);
+  row_quant_store<V>(a, amax, n, q + row * n, s + row);
 }
+
+// Register-resident row width: the smallest V in {1, 2, 4, 8} with n <= 8192 V.
+inline int row_vectors(int n) { return n <= 8192 ? 1 : n <= 16384 ? 2 : n <= 32768 ? 4 : 8; }
+constexpr int kRowMaxN = 8 * kRowThreads * 8;
 
 bool act_dtype_ok(int dt) { return dt == TI_DTYPE_F16 || dt == TI_DTYPE_BF16; }
 
@@ -331,22 +350,35 @@ extern "C" int ti_fp8_quant_tensor(const void* x, int x_dtype, long n, const flo
 extern "C" int ti_fp8_rmsnorm_quant_per_token(const void* x, const void* residual, const void* weight, int dtype,
                                               int rows, int n, float eps, void* hidden_out, uint8_t* xq, float* xs,
                                               hipStream_t stream) {
+  using namespace ti::fp8;
   TI_CHECK_ARG(x && weight && xq && xs && (!residual || hidden_out), "ti_fp8_rmsnorm_quant_per_token: null pointer");
   TI_CHECK_ARG(act_dtype_ok(dtype), "ti_fp8_rmsnorm_quant_per_token: dtype must be fp16 or bf16");
-  TI_CHECK_SHAPE(rows >= 0 && n > 0 && n % 8 == 0, "ti_fp8_rmsnorm_quant_per_token: need n %% 8 == 0 (n=%d)", n);
+  TI_CHECK_SHAPE(rows >= 0 && n > 0 && n % 8 == 0 && n <= kRowMaxN,
+                 "ti_fp8_rmsnorm_quant_per_token: need n %% 8 == 0 and n <= %d (n=%d)", kRowMaxN, n);
   TI_CHECK_ARG(((uintptr_t)x & 15) == 0 && ((uintptr_t)weight & 15) == 0 && ((uintptr_t)xq & 7) == 0 &&
                    (!residual || (((uintptr_t)residual & 15) == 0 && ((uintptr_t)hidden_out & 15) == 0)),
                "ti_fp8_rmsnorm_quant_per_token: misaligned pointer");
   if (rows == 0) return TI_OK;
-#define TI_RQ(DT, ADD)                                                                                         \
-  hipLaunchKernelGGL((rmsnorm_quant_kernel<DT, ADD>), dim3(rows), dim3(256), 0, stream, (const uint16_t*)x,   \
-                     (const uint16_t*)residual, (const uint16_t*)weight, n, eps, (uint16_t*)hidden_out, xq, xs)
+  const int v = row_vectors(n);
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(rows), dim3(kRowThreads), 0, stream, (const uint16_t*)x, (const uint16_t*)residual,
+                       (const uint16_t*)weight, n, eps, (uint16_t*)hidden_out, xq, xs);
+  };
+  auto by_v = [&](auto dt, auto add) {
+    constexpr int DT = decltype(dt)::value;
+    constexpr bool ADD = decltype(add)::value;
+    if (v == 1) launch(rmsnorm_quant_kernel<DT, 1, ADD>);
+    else if (v == 2) launch(rmsnorm_quant_kernel<DT, 2, ADD>);
+    else if (v == 4) launch(rmsnorm_quant_kernel<DT, 4, ADD>);
+    else launch(rmsnorm_quant_kernel<DT, 8, ADD>);
+  };
+  using F16 = std::integral_constant<int, TI_DTYPE_F16>;
+  using BF16 = std::integral_constant<int, TI_DTYPE_BF16>;
   if (dtype == TI_DTYPE_F16) {
-    if (residual) TI_RQ(TI_DTYPE_F16, true); else TI_RQ(TI_DTYPE_F16, false);
+    if (residual) by_v(F16{}, std::true_type{}); else by_v(F16{}, std::false_type{});
   } else {
-    if (residual) TI_RQ(TI_DTYPE_BF16, true); else TI_RQ(TI_DTYPE_BF16, false);
+    if (residual) by_v(BF16{}, std::true_type{}); else by_v(BF16{}, std::false_type{});
   }
-#undef TI_RQ
   TI_CHECK_LAUNCH("ti_fp8_rmsnorm_quant_per_token");
   return TI_OK;
 }
@@ -354,19 +386,29 @@ extern "C" int ti_fp8_rmsnorm_quant_per_token(const void* x, const void* residua
 extern "C" int ti_fp8_swiglu_quant_per_token(const void* gate, long gate_row_stride, const void* up,
                                              long up_row_stride, int dtype, int rows, int n, uint8_t* xq, float* xs,
                                              hipStream_t stream) {
+  using namespace ti::fp8;
   TI_CHECK_ARG(gate && up && xq && xs, "ti_fp8_swiglu_quant_per_token: null pointer");
   TI_CHECK_ARG(act_dtype_ok(dtype), "ti_fp8_swiglu_quant_per_token: dtype must be fp16 or bf16");
-  TI_CHECK_SHAPE(rows >= 0 && n > 0 && n % 8 == 0 && gate_row_stride % 8 == 0 && up_row_stride % 8 == 0,
-                 "ti_fp8_swiglu_quant_per_token: need n and row strides %% 8 == 0 (n=%d)", n);
+  TI_CHECK_SHAPE(rows >= 0 && n > 0 && n % 8 == 0 && n <= kRowMaxN && gate_row_stride % 8 == 0 &&
+                     up_row_stride % 8 == 0,
+                 "ti_fp8_swiglu_quant_per_token: need n and row strides %% 8 == 0 and n <= %d (n=%d)", kRowMaxN, n);
   TI_CHECK_ARG(((uintptr_t)gate & 15) == 0 && ((uintptr_t)up & 15) == 0 && ((uintptr_t)xq & 7) == 0,
                "ti_fp8_swiglu_quant_per_token: misaligned pointer");
   if (rows == 0) return TI_OK;
-  if (dtype == TI_DTYPE_F16)
-    hipLaunchKernelGGL(swiglu_quant_kernel<TI_DTYPE_F16>, dim3(rows), dim3(256), 0, stream, (const uint16_t*)gate,
-                       gate_row_stride, (const uint16_t*)up, up_row_stride, n, xq, xs);
-  else
-    hipLaunchKernelGGL(swiglu_quant_kernel<TI_DTYPE_BF16>, dim3(rows), dim3(256), 0, stream, (const uint16_t*)gate,
-                       gate_row_stride, (const uint16_t*)up, up_row_stride, n, xq, xs);
+  const int v = row_vectors(n);
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(rows), dim3(kRowThreads), 0, stream, (const uint16_t*)gate, gate_row_stride,
+                       (const uint16_t*)up, up_row_stride, n, xq, xs);
+  };
+  auto by_v = [&](auto dt) {
+    constexpr int DT = decltype(dt)::value;
+    if (v == 1) launch(swiglu_quant_kernel<DT, 1>);
+    else if (v == 2) launch(swiglu_quant_kernel<DT, 2>);
+    else if (v == 4) launch(swiglu_quant_kernel<DT, 4>);
+    else launch(swiglu_quant_kernel<DT, 8>);
+  };
+  if (dtype == TI_DTYPE_F16) by_v(std::integral_constant<int, TI_DTYPE_F16>{});
+  else by_v(std::integral_constant<int, TI_DTYPE_BF16>{});
   TI_CHECK_LAUNCH("ti_fp8_swiglu_quant_per_token");
   return TI_OK;
 }

@@ -12,9 +12,10 @@ from ``torchinferno.kernels.triton_ops`` (tensor_parallel.py:3073-3187):
 
 Same arguments, output shapes (``q`` viewed like the input, ``scale [rows, 1]``
 fp32) and ``ValueError`` checks; the ``triton_*`` names are aliases.  Each is one
-libti_quant.so launch (one workgroup per row): the row is read from HBM once per
-pass and only the e4m3 codes, the scale and (add variant) the summed hidden
-state are written.  Unlike the reference there is no 8192-column limit.
+libti_quant.so launch, one 1024-thread workgroup per row with the row held in
+registers: each input byte is read from HBM once, and only the e4m3 codes, the
+scale and (add variant) the summed hidden state are written.  Widths up to 65536
+(the reference stops at 8192).
 
 The norm's weight is read in the activation dtype (a weight of another dtype is
 cast first).  Roundings are fixed: fp64 sum of squares rounded once to fp32,
@@ -28,6 +29,7 @@ from torch import Tensor
 from .. import _lib
 
 _ACT = (torch.bfloat16, torch.float16)
+MAX_WIDTH = 65536  # a row is held in one workgroup's registers
 
 
 def _outputs(x: Tensor) -> tuple[Tensor, Tensor, int, int]:
@@ -38,6 +40,8 @@ def _outputs(x: Tensor) -> tuple[Tensor, Tensor, int, int]:
     rows = x.numel() // n if n else 0
     if n % 8:
         raise ValueError("per-token FP8 fusion requires a width divisible by 8")
+    if n > MAX_WIDTH:
+        raise ValueError(f"per-token FP8 fusion supports widths up to {MAX_WIDTH}")
     q = torch.empty((rows, n), dtype=torch.float8_e4m3fn, device=x.device)
     s = torch.empty((rows, 1), dtype=torch.float32, device=x.device)
     return q, s, rows, n
