@@ -185,3 +185,14 @@ def test_decode_kernel_tall_tiles(dev, monkeypatch, plan, mr, m):
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_PLAN", plan)
     out, ref = _run_gemm(dev, m, 2048, 512, torch.float16 if m % 2 else torch.bfloat16, 30 + m)
     assert _rel_err(out.float().cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("m", [5, 8, 16])
+def test_decode_four_row_override_ignored_above_four_rows(dev, monkeypatch, m):
+    """A forced 4-row tile (TI_ROCM_W4A16_DECODE_MR=4) stages only 4 activation
+    rows, so the plan keeps it for M <= 4 only; larger M falls back to 16 rows."""
+    print(f"[int4] decode MR=4 override M={m}", flush=True)
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MIN_M", "1")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MR", "4")
+    out, ref = _run_gemm(dev, m, 2048, 512, torch.bfloat16, 50 + m)
+    assert _rel_err(out.float().cpu().numpy(), ref) <= TOL

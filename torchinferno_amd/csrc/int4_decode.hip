@@ -314,7 +314,8 @@ DecodePlan make_decode_plan(int M, int N, int K) {
   const char* emr = getenv("TI_ROCM_W4A16_DECODE_MR");
   if (emr && *emr) {
     const int v = atoi(emr);
-    if (v == 4 || v == 16 || v == 32 || v == 64 || v == 128) p.mr = v;
+    // 4-row tiles stage only 4 activation rows: valid for M <= 4 alone.
+    if ((v == 4 && M <= 4) || v == 16 || v == 32 || v == 64 || v == 128) p.mr = v;
   }
   const bool tall = p.mr >= 64;
   p.mchunks = cdiv(M, p.mr > 16 ? p.mr : 16);
