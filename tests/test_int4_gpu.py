@@ -179,6 +179,7 @@ _TALL_PLANS = ["2:2:2:1", "4:1:2:1", "4:1:3:2", "2:1:3:1", "2:1:4:3", "2:1:2:1",
 @pytest.mark.parametrize("mr,m", [(64, 40), (64, 100), (128, 77), (128, 128), (128, 200)])
 def test_decode_kernel_tall_tiles(dev, monkeypatch, plan, mr, m):
     print(f"[int4] tall plan {plan} MR={mr} M={m}", flush=True)
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_WAVES", "4")
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MIN_M", "1")
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MAX_M", "4096")
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MR", str(mr))
@@ -195,4 +196,19 @@ def test_decode_four_row_override_ignored_above_four_rows(dev, monkeypatch, m):
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MIN_M", "1")
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MR", "4")
     out, ref = _run_gemm(dev, m, 2048, 512, torch.bfloat16, 50 + m)
+    assert _rel_err(out.float().cpu().numpy(), ref) <= TOL
+
+
+# 8-wave tall tiles (64 rows, K halves on two waves per SIMD): each instantiated
+# (nt, ring), with and without split-K, ragged M, both dtypes, narrow and wide N.
+@pytest.mark.parametrize("plan", ["4:2:2:1", "4:2:2:3", "2:2:2:1", "2:2:3:1", "2:2:3:2"])
+@pytest.mark.parametrize("m,n", [(40, 512), (64, 1024), (100, 768), (128, 512)])
+def test_decode_kernel_eight_waves(dev, monkeypatch, plan, m, n):
+    print(f"[int4] 8-wave plan {plan} M={m} N={n}", flush=True)
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MIN_M", "1")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MAX_M", "4096")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MR", "64")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_WAVES", "8")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_PLAN", plan)
+    out, ref = _run_gemm(dev, m, 2048, n, torch.float16 if m % 2 else torch.bfloat16, 60 + m)
     assert _rel_err(out.float().cpu().numpy(), ref) <= TOL

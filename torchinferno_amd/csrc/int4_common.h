@@ -120,5 +120,6 @@ __device__ __forceinline__ void compute_group_rows(const i32x4 (&w)[NT], GetA&& 
     }
   }
 }
+
 }  // namespace int4
 }  // namespace ti

@@ -12,7 +12,8 @@ constexpr int kDecodeLdsMax = 160 * 1024 - 256;  // gfx950 LDS per workgroup, le
 struct DecodePlan {
   int mr;       // activation rows staged per K range and stage (4, 16, 32, 64, 128)
   int nt;       // 16-column tiles per wave
-  int wk;       // waves splitting K inside the workgroup (of 4)
+  int wk;       // waves splitting K inside the workgroup
+  int waves;    // waves per workgroup (4, or 8 for tall tiles: two per SIMD)
   int ring;     // LDS ring stages
   int splits;   // K splits across workgroups
   int mchunks;  // row chunks (grid z)

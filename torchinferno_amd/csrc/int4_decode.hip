@@ -35,19 +35,19 @@ namespace {
 
 constexpr int kWaves = 4;
 
-template <int DT, int MR, int NT, int WK, int R, int SPLIT>
-__global__ __launch_bounds__(64 * kWaves) void w4a16_decode_kernel(
+template <int DT, int MR, int NT, int WK, int R, int SPLIT, int KW>
+__global__ __launch_bounds__(64 * KW) void w4a16_decode_kernel(
     const uint16_t* __restrict__ A, const i32x4* __restrict__ Wp, const uint16_t* __restrict__ Sg,
     uint16_t* __restrict__ out, float* __restrict__ partial, int* __restrict__ tickets, int M, int N,
     int K, int splits) {
-  constexpr int WN = kWaves / WK;
+  constexpr int WN = KW / WK;
   constexpr int MT = MR > 16 ? MR / 16 : 1;      // 16-row MFMA tiles
   constexpr int MP = MT * 16;                    // rows of one row chunk
   constexpr int AI = WK * MR / 4;                // 1 KiB activation DMAs per stage (all waves)
-  constexpr int AI_LO = AI / kWaves;             // ... per wave: AI_LO or AI_HI
-  constexpr int AI_HI = (AI + kWaves - 1) / kWaves;
+  constexpr int AI_LO = AI / KW;             // ... per wave: AI_LO or AI_HI
+  constexpr int AI_HI = (AI + KW - 1) / KW;
   constexpr int P = R - 1;                       // stages in flight ahead of compute
-  constexpr int W_BYTES = kWaves * NT * 1024;    // weight blocks of one stage
+  constexpr int W_BYTES = KW * NT * 1024;    // weight blocks of one stage
   constexpr int A_BYTES = MR * 256;              // one K range's activations of one stage
   constexpr int STAGE = W_BYTES + WK * A_BYTES;
   constexpr int WC = WN * NT * 16;               // columns of the workgroup
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_decode_kernel(
   const long T = N / 16;
   const int m0 = mchunk * MP;
   // Activation DMAs of this wave: ids wave, wave + 4, ... below AI.
-  const int a_cnt = (AI - wave + kWaves - 1) / kWaves;
+  const int a_cnt = (AI - wave + KW - 1) / KW;
   const int col_base = nb * WC;
   const long tile0 = (long)nb * (WN * NT) + wn * NT;
 
@@ -85,7 +85,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_decode_kernel(
   {
     const int sbytes = ngr * WC * 2;
     const int nch = cdiv(sbytes, 256);
-    for (int ch = wave; ch < nch; ch += kWaves) {
+    for (int ch = wave; ch < nch; ch += KW) {
       const int o = ch * 256 + lane * 4;
       const uint16_t* src = Sg;
       if (o < sbytes) {
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_decode_kernel(
       dma16(&Wp[((long)g * T + tile0 + t) * 64 + lane], base + (uint32_t)((wave * NT + t) * 1024));
 #pragma unroll
     for (int u = 0; u < AI_HI; ++u) {
-      const int id = wave + u * kWaves;        // 0 .. AI - 1
+      const int id = wave + u * KW;        // 0 .. AI - 1
       if (id >= AI) break;
       const int awk = id / (MR / 4), k4 = id % (MR / 4);
       const int r = 4 * k4 + (lane >> 4);
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_decode_kernel(
     last_flag = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
   __syncthreads();
   if (!last_flag) return;
-  for (int e = threadIdx.x; e < rows * WC; e += 64 * kWaves) {
+  for (int e = threadIdx.x; e < rows * WC; e += 64 * KW) {
     const int r = e / WC;
     const long off = (long)(m0 + r) * N + col_base + e % WC;
     float v = 0.f;
@@ -233,14 +233,14 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_decode_kernel(
   if (threadIdx.x == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int DT, int MR, int NT, int WK, int R>
+template <int DT, int MR, int NT, int WK, int R, int KW = kWaves>
 void launch_split(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
   dim3 grid(p.nblocks, p.splits, p.mchunks);
   if (p.splits == 1)
-    hipLaunchKernelGGL((w4a16_decode_kernel<DT, MR, NT, WK, R, 0>), grid, dim3(64 * kWaves), p.lds,
+    hipLaunchKernelGGL((w4a16_decode_kernel<DT, MR, NT, WK, R, 0, KW>), grid, dim3(64 * KW), p.lds,
                        stream, x.a, x.w, x.s, x.out, x.partial, x.tickets, x.M, x.N, x.K, 1);
   else
-    hipLaunchKernelGGL((w4a16_decode_kernel<DT, MR, NT, WK, R, 2>), grid, dim3(64 * kWaves), p.lds,
+    hipLaunchKernelGGL((w4a16_decode_kernel<DT, MR, NT, WK, R, 2, KW>), grid, dim3(64 * KW), p.lds,
                        stream, x.a, x.w, x.s, x.out, x.partial, x.tickets, x.M, x.N, x.K, p.splits);
 }
 
@@ -266,11 +266,18 @@ void launch_nt(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
 }
 
 // Tall tiles (64 / 128 staged rows) instantiate a curated set of
-// (nt, wk, ring) configurations -- (2,2,2), (4,1,2|3), (2,1,2|3|4); the plan
-// only produces these.
+// (nt, wk, ring) configurations -- 4 waves: (2,2,2), (4,1,2|3), (2,1,2|3|4);
+// 8 waves (two per SIMD, K split in halves, 64-row tiles only -- 128 rows do
+// not fit two stages): (4,2,2), (2,2,2|3); the plan only produces these.
 template <int DT, int MR>
 void launch_tall(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
-  if (p.wk == 2) launch_split<DT, MR, 2, 2, 2>(p, x, stream);
+  if (MR == 64 && p.waves == 8) {
+    if constexpr (MR == 64) {
+      if (p.nt == 4) launch_split<DT, MR, 4, 2, 2, 8>(p, x, stream);
+      else if (p.ring == 2) launch_split<DT, MR, 2, 2, 2, 8>(p, x, stream);
+      else launch_split<DT, MR, 2, 2, 3, 8>(p, x, stream);
+    }
+  } else if (p.wk == 2) launch_split<DT, MR, 2, 2, 2>(p, x, stream);
   else if (p.nt == 4) {
     if (p.ring == 2) launch_split<DT, MR, 4, 1, 2>(p, x, stream);
     else launch_split<DT, MR, 4, 1, 3>(p, x, stream);
@@ -290,7 +297,7 @@ void launch_mr(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
   else launch_tall<DT, 128>(p, x, stream);
 }
 
-int stage_bytes(int mr, int nt, int wk) { return kWaves * nt * 1024 + wk * mr * 256; }
+int stage_bytes(int mr, int nt, int wk, int waves) { return waves * nt * 1024 + wk * mr * 256; }
 
 // TI_ROCM_W4A16_DECODE_PLAN="nt:wk:ring:splits" overrides the heuristic (tuning).
 bool env_plan(DecodePlan& p) {
@@ -302,15 +309,59 @@ bool env_plan(DecodePlan& p) {
   return true;
 }
 
+// Completes a plan: snaps (nt, wk, ring) to an instantiated configuration,
+// tiles N, caps splits and sizes the LDS (ring, staged scales, WK reduction).
+DecodePlan finish_decode_plan(DecodePlan p, int N, int NG, bool tall) {
+  if (tall && p.waves == 8) {
+    // 8 waves = 2 K halves x 4 column sets: (4,2,2) covers 256 columns,
+    // (2,2,2|3) 128.
+    p.wk = 2;
+    if (p.nt >= 4 && N % 256 == 0) { p.nt = 4; p.ring = 2; }
+    else { p.nt = 2; p.ring = p.ring >= 3 ? 3 : 2; }
+    if (N % (4 * p.nt * 16)) { p.waves = kWaves; p.wk = 1; }  // the 4-wave table below
+  }
+  if (tall && p.waves != 8) {
+    // The instantiated tall configurations: (2,2,2), (4,1,2|3), (2,1,2|3|4); a
+    // workgroup covers 256 / 128 / 64 columns, which must divide N.
+    if (p.wk == 1 && p.nt >= 4 && N % 256) p.nt = 2;
+    if (p.wk == 1 && p.nt < 4 && N % 128) p.wk = 2;
+    if (p.wk != 1) { p.wk = 2; p.nt = 2; p.ring = 2; }
+    else if (p.nt >= 4) { p.nt = 4; p.ring = p.ring <= 2 ? 2 : 3; }
+    else { p.nt = 2; p.ring = p.ring >= 4 ? 4 : (p.ring <= 2 ? 2 : 3); }
+  } else if (!tall) {
+    if (p.nt != 1 && p.nt != 2 && p.nt != 4) p.nt = 2;
+    if (p.wk != 1 && p.wk != 2 && p.wk != 4) p.wk = 1;
+    if (p.ring != 3 && p.ring != 4 && p.ring != 6) p.ring = 4;
+    while (p.nt > 1 && N % (kWaves / p.wk * p.nt * 16)) p.nt /= 2;
+    while (p.wk < 4 && N % (kWaves / p.wk * p.nt * 16)) p.wk *= 2;
+  }
+  p.nblocks = N / (p.waves / p.wk * p.nt * 16);
+  p.splits = max(1, min(p.splits, max(1, NG / (2 * p.wk))));
+  const int ngr = cdiv(NG, p.splits);
+  const int wc = p.waves / p.wk * p.nt * 16;
+  const int sbytes = cdiv(ngr * wc * 2, 256) * 256;
+  auto fits = [&](int r) { return r * stage_bytes(p.mr, p.nt, p.wk, p.waves) + sbytes <= kDecodeLdsMax; };
+  if (tall) {
+    while (p.ring > 2 && !fits(p.ring)) p.ring = p.ring == 4 ? 3 : 2;
+  } else {
+    while (p.ring > 3 && !fits(p.ring)) p.ring = p.ring == 6 ? 4 : 3;
+  }
+  const int stage = p.ring * stage_bytes(p.mr, p.nt, p.wk, p.waves) + sbytes;
+  const int mt = p.mr >= 16 ? p.mr / 16 : 1;
+  const int red = (p.wk - 1) * (p.waves / p.wk) * p.nt * mt * 256 * 4;
+  p.lds = stage > red ? stage : red;
+  return p;
+}
+
 }  // namespace
 
 DecodePlan make_decode_plan(int M, int N, int K) {
   DecodePlan p;
   const int T = N / 16;
   const bool wide = T >= 1024;
-  // Staged rows: M's own size up to 32; beyond, 32-row chunks, except wide N
-  // above 64 rows, where 64-row tiles (half the weight re-reads) win.
-  p.mr = M <= 4 ? 4 : (M <= 16 ? 16 : (M <= 64 || !wide ? 32 : 64));
+  // Staged rows: M's own size up to 32; beyond, 32-row chunks for narrow N and
+  // 64-row tiles (half the weight re-reads) for wide N.
+  p.mr = M <= 4 ? 4 : (M <= 16 ? 16 : ((M <= 32 || !wide) ? 32 : 64));
   const char* emr = getenv("TI_ROCM_W4A16_DECODE_MR");
   if (emr && *emr) {
     const int v = atoi(emr);
@@ -319,6 +370,10 @@ DecodePlan make_decode_plan(int M, int N, int K) {
   }
   const bool tall = p.mr >= 64;
   p.mchunks = cdiv(M, p.mr > 16 ? p.mr : 16);
+  // Wide N above 32 rows: 64-row tiles on 8 waves (two per SIMD, the K range
+  // halved between them) -- measured 17% (M=64) / 7% (M=128) faster than the
+  // best 4-wave plans at the Llama-3-8B gate_up shape.
+  p.waves = (p.mr == 64 && wide) ? 8 : kWaves;
   const int NG = K / kGroup;
   if (!env_plan(p)) {
     // Measured on MI355X at the Llama-3-8B MLP shapes, rows 17..128: wide N
@@ -327,7 +382,7 @@ DecodePlan make_decode_plan(int M, int N, int K) {
     p.splits = 1;
     p.ring = 3;
     if (tall) {
-      p.nt = 4; p.wk = 1; p.ring = 2;
+      p.nt = (p.waves == 8 && M <= 64) ? 2 : 4; p.wk = 1; p.ring = 2;
       const int blocks = max(1, cdiv(T, kWaves * p.nt)) * p.mchunks;
       p.splits = blocks >= 192 ? 1 : cdiv(256, blocks);
     } else if (wide) {
@@ -340,43 +395,29 @@ DecodePlan make_decode_plan(int M, int N, int K) {
       p.splits = (M <= 32 && blocks * p.mchunks < 256) ? 2 : 1;
     }
   }
-  if (tall) {
-    // The instantiated tall configurations: (2,2,2), (4,1,2|3), (2,1,2|3|4); a
-    // workgroup covers 256 / 128 / 64 columns, which must divide N.
-    if (p.wk == 1 && p.nt >= 4 && N % 256) p.nt = 2;
-    if (p.wk == 1 && p.nt < 4 && N % 128) p.wk = 2;
-    if (p.wk != 1) { p.wk = 2; p.nt = 2; p.ring = 2; }
-    else if (p.nt >= 4) { p.nt = 4; p.ring = p.ring <= 2 ? 2 : 3; }
-    else { p.nt = 2; p.ring = p.ring >= 4 ? 4 : (p.ring <= 2 ? 2 : 3); }
-  } else {
-    if (p.nt != 1 && p.nt != 2 && p.nt != 4) p.nt = 2;
-    if (p.wk != 1 && p.wk != 2 && p.wk != 4) p.wk = 1;
-    if (p.ring != 3 && p.ring != 4 && p.ring != 6) p.ring = 4;
+  const char* ew = getenv("TI_ROCM_W4A16_DECODE_WAVES");
+  if (ew && *ew && p.mr == 64) p.waves = atoi(ew) == 8 ? 8 : kWaves;
+  DecodePlan q = finish_decode_plan(p, N, NG, tall);
+  // An 8-wave plan whose LDS (ring + the staged scale slab, which grows with
+  // K) does not fit steps down to 128 columns, then to the 4-wave table.
+  if (q.waves == 8 && q.lds > kDecodeLdsMax && q.nt == 4) {
+    p.nt = 2;
+    q = finish_decode_plan(p, N, NG, tall);
   }
-  if (!tall) {
-    while (p.nt > 1 && N % (kWaves / p.wk * p.nt * 16)) p.nt /= 2;
-    while (p.wk < 4 && N % (kWaves / p.wk * p.nt * 16)) p.wk *= 2;
+  if (q.waves == 8 && q.lds > kDecodeLdsMax) {
+    p.waves = kWaves;
+    p.wk = 1;
+    q = finish_decode_plan(p, N, NG, tall);
   }
-  p.nblocks = N / (kWaves / p.wk * p.nt * 16);
-  p.splits = max(1, min(p.splits, max(1, NG / (2 * p.wk))));
-  const int ngr = cdiv(NG, p.splits);
-  const int wc = kWaves / p.wk * p.nt * 16;
-  const int sbytes = cdiv(ngr * wc * 2, 256) * 256;
-  auto fits = [&](int r) { return r * stage_bytes(p.mr, p.nt, p.wk) + sbytes <= kDecodeLdsMax; };
-  if (tall) {
-    while (p.ring > 2 && !fits(p.ring)) p.ring = p.ring == 4 ? 3 : 2;
-  } else {
-    while (p.ring > 3 && !fits(p.ring)) p.ring = p.ring == 6 ? 4 : 3;
-  }
-  const int stage = p.ring * stage_bytes(p.mr, p.nt, p.wk) + sbytes;
-  const int mt = p.mr >= 16 ? p.mr / 16 : 1;
-  const int red = (p.wk - 1) * (kWaves / p.wk) * p.nt * mt * 256 * 4;
-  p.lds = stage > red ? stage : red;
-  return p;
+  return q;
 }
 
 bool decode_plan_valid(const DecodePlan& p, int N) {
-  if (N % (kWaves / p.wk * p.nt * 16) || p.nblocks * (kWaves / p.wk * p.nt * 16) != N) return false;
+  if (p.waves != 4 && p.waves != 8) return false;
+  if (N % (p.waves / p.wk * p.nt * 16) || p.nblocks * (p.waves / p.wk * p.nt * 16) != N) return false;
+  if (p.lds > kDecodeLdsMax) return false;
+  if (p.waves == 8)
+    return p.mr == 64 && p.wk == 2 && ((p.nt == 4 && p.ring == 2) || (p.nt == 2 && (p.ring == 2 || p.ring == 3)));
   if (p.mr >= 64)
     return (p.nt == 2 && p.wk == 2 && p.ring == 2) || (p.nt == 4 && p.wk == 1 && (p.ring == 2 || p.ring == 3)) ||
            (p.nt == 2 && p.wk == 1 && (p.ring >= 2 && p.ring <= 4));

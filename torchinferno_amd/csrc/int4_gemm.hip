@@ -569,8 +569,8 @@ extern "C" int ti_w4a16_plan_name(int M, int N, int K, int group_size, char* buf
                  "ti_w4a16_plan_name: need M >= 1, K %% 128 == 0, N %% 64 == 0");
   if (use_decode(M)) {
     DecodePlan d = make_decode_plan(M, N, K);
-    snprintf(buf, len, "w4a16_decode_kernel mr=%d nt=%d wk=%d ring=%d splits=%d mchunks=%d lds=%d", d.mr, d.nt, d.wk,
-             d.ring, d.splits, d.mchunks, d.lds);
+    snprintf(buf, len, "w4a16_decode_kernel mr=%d nt=%d wk=%d waves=%d ring=%d splits=%d mchunks=%d lds=%d", d.mr,
+             d.nt, d.wk, d.waves, d.ring, d.splits, d.mchunks, d.lds);
     TI_CHECK_SHAPE(d.lds <= kDecodeLdsMax && decode_plan_valid(d, N), "ti_w4a16_plan_name: invalid plan (%s)", buf);
   } else {
     Plan p = make_plan(M, N, K);
