@@ -162,7 +162,8 @@ int ti_fp8_swiglu_quant_per_token(const void* gate, long gate_row_stride, const 
  * Skinny M may split K across workgroups: pass a workspace of
  * ti_fp8_gemm_workspace_bytes() (zero-filled once when allocated; every call
  * leaves its ticket words zero again; calls sharing one workspace must be
- * stream-ordered).  scale_mode: 0 = row/column scales, 1 = 128x128 blocks.
+ * stream-ordered).  scale_mode: 0 = row/column scales, 1 = 128x128 blocks,
+ * 2 = MXFP4 weights (ti_fp4_gemm).
  * ------------------------------------------------------------------------- */
 size_t ti_fp8_gemm_workspace_bytes(int M, int N, int K, int scale_mode);
 size_t ti_fp8_gemm_workspace_bytes_max(int max_m, int N, int K, int scale_mode);
@@ -185,6 +186,17 @@ int ti_fp8_gemm_rowcol(const uint8_t* a, const float* a_scale, int a_scale_per_r
 int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, const uint8_t* b,
                       const float* b_scale, void* out, int out_dtype, int M, int N, int K,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* FP8 activations x MXFP4 weights: out[m,n] = sum_k a[m,k] * a_scale[m, k/128]
+ * * w[n,k] * 2^(b_scale[n, k/32] - 127).  a e4m3 [M,K] with fp32 1x128 scales
+ * [M, K/128]; b e2m1 [N, K/2] (two values per byte along K, element 2i in the
+ * low nibble -- torch float4_e2m1fn_x2); b_scale E8M0 bytes [N, K/32]; the
+ * e8m0 scales are applied inside the MFMA (gfx950 block-scaled f8f6f4).
+ * Replaces fp4_gemm (src/torchinferno/kernels/deepseek_v4_tilelang.py,
+ * kernel deepseek_v4_tilelang_definitions.py:674-769).  K % 128 == 0. */
+int ti_fp4_gemm(const uint8_t* a, const float* a_scale, const uint8_t* b, const uint8_t* b_scale,
+                void* out, int out_dtype, int M, int N, int K, void* workspace, size_t workspace_bytes,
+                hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Routed FP8 block-scaled MoE (DeepSeek expert shapes).
@@ -218,6 +230,18 @@ size_t ti_fp8_moe_workspace_bytes(int T, int k, int E, int H, int I);
 int ti_fp8_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids,
                int T, int k, const uint8_t* w13, const float* s13, const uint8_t* w2,
                const float* s2, int E, int H, int I, float clamp_limit, void* out,
+               void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* The same routed experts with MXFP4 weights (DSv4 expert_dtype "fp4"): every
+ * w*_e is an e2m1 Linear with E8M0 scales per 32 K, applied as ti_fp4_gemm
+ * (1x128 FP8 activations) -- the arithmetic of the reference's "tilelang-mxfp4"
+ * expert path (Expert -> linear -> act_quant + fp4_gemm, tensor_parallel.py:
+ * 195-207).  Replaces fused_mxfp4_moe (deepseek_v4_marlin.py:311-411).
+ *   w13 e2m1 [E, 2I, H/2], s13 E8M0 [E, 2I, H/32]; w2 e2m1 [E, H, I/2],
+ *   s2 E8M0 [E, H, I/32]; workspace as ti_fp8_moe_workspace_bytes. */
+int ti_fp4_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids,
+               int T, int k, const uint8_t* w13, const uint8_t* s13, const uint8_t* w2,
+               const uint8_t* s2, int E, int H, int I, float clamp_limit, void* out,
                void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus

@@ -30,6 +30,7 @@ from __future__ import annotations
 
 import numpy as np
 
+from .fp4 import fp4_gemm
 from .fp8 import act_quant_block, fp8_gemm_block
 from .numerics import bf16_round
 
@@ -56,21 +57,28 @@ def block_fp8_linear(x_bf16: np.ndarray, w_codes: np.ndarray, w_s: np.ndarray) -
     return bf16_round(fp8_gemm_block(xq, xs, w_codes, w_s))
 
 
+def mxfp4_linear(x_bf16: np.ndarray, w_packed: np.ndarray, w_s: np.ndarray) -> np.ndarray:
+    """DSv4 ``linear`` for an MXFP4 weight: act_quant 1x128 then fp4_gemm, bf16 out."""
+    xq, xs = act_quant_block(x_bf16)
+    return bf16_round(fp4_gemm(xq, xs, w_packed, w_s))
+
+
 def expert_forward(x_bf16: np.ndarray, route_w: np.ndarray, w13: np.ndarray, s13: np.ndarray,
-                   w2: np.ndarray, s2: np.ndarray) -> np.ndarray:
-    """One expert on its routed rows.  x bf16-valued [R,H], route_w [R,1]."""
+                   w2: np.ndarray, s2: np.ndarray, linear=block_fp8_linear) -> np.ndarray:
+    """One expert on its routed rows.  x bf16-valued [R,H], route_w [R,1];
+    ``linear`` is the weight format's Linear (block FP8 or MXFP4)."""
     inter = w13.shape[0] // 2
-    gu = block_fp8_linear(x_bf16, w13, s13)  # [R, 2I] bf16 values
+    gu = linear(x_bf16, w13, s13)  # [R, 2I] bf16 values
     gate, up = gu[:, :inter], gu[:, inter:]
     sig = (1.0 / (1.0 + np.exp(-gate.astype(np.float64)))).astype(F32)
     h = (gate * sig).astype(F32) * up  # F.silu(gate) * up in fp32
     h = (route_w.astype(F32) * h).astype(F32)
-    return block_fp8_linear(bf16_round(h), w2, s2)
+    return linear(bf16_round(h), w2, s2)
 
 
 def moe_reference(x_bf16: np.ndarray, weights: np.ndarray, ids: np.ndarray,
-                  experts: list[tuple[np.ndarray, np.ndarray, np.ndarray, np.ndarray]]
-                  ) -> np.ndarray:
+                  experts: list[tuple[np.ndarray, np.ndarray, np.ndarray, np.ndarray]],
+                  linear=block_fp8_linear) -> np.ndarray:
     """Per-expert loop; returns fp32 values rounded to bf16, [T,H]."""
     t, h = x_bf16.shape
     y = np.zeros((t, h), dtype=F32)
@@ -78,6 +86,6 @@ def moe_reference(x_bf16: np.ndarray, weights: np.ndarray, ids: np.ndarray,
         tok, slot = np.nonzero(ids == e)
         if tok.size == 0:
             continue
-        out = expert_forward(x_bf16[tok], weights[tok, slot][:, None], w13, s13, w2, s2)
+        out = expert_forward(x_bf16[tok], weights[tok, slot][:, None], w13, s13, w2, s2, linear)
         np.add.at(y, tok, out)
     return bf16_round(y)

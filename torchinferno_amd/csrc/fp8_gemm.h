@@ -12,7 +12,8 @@ struct GemmArgs {
   const uint8_t* a;   // [M, K] e4m3
   const uint8_t* b;   // [N, K] e4m3
   const float* sa;    // row scales (SMODE 0, stride sa_stride) or [M, K/128] (SMODE 1)
-  const float* sb;    // column scales (SMODE 0, stride sb_stride) or [ceil(N/128), K/128]
+  const float* sb;    // column scales (SMODE 0, stride sb_stride), [ceil(N/128), K/128] (SMODE 1),
+                      // or e8m0 bytes [N, K/32] (SMODE 2)
   int sa_stride, sb_stride;
   uint16_t* out;      // [M, N] bf16 / fp16
   float* partial;     // split-K fp32 partials [splits][M][N]
@@ -28,7 +29,7 @@ struct GemmArgs {
   const int* tile_rows;     // rows of each m-tile (<= BM)
   const int* num_mtiles;    // device scalar: m-tiles in use
   long b_expert_stride;     // bytes between experts' [N, K] weights
-  long sb_expert_stride;    // floats between experts' weight-scale grids
+  long sb_expert_stride;    // 4-byte units between experts' weight-scale grids
 };
 
 struct GemmPlan {
@@ -47,7 +48,7 @@ void launch_gemm(const GemmPlan& p, int smode, int odt, const GemmArgs& x, hipSt
 // of 2 (128x128), 5 (64x128), 6 (16x128), 9 (256x128).
 int grouped_bm(int kind);
 int grouped_bn(int kind);
-void launch_gemm_grouped(int kind, const GemmArgs& x, int max_mtiles, hipStream_t stream);
+void launch_gemm_grouped(int kind, int smode, const GemmArgs& x, int max_mtiles, hipStream_t stream);
 
 }  // namespace fp8
 }  // namespace ti

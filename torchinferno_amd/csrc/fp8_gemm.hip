@@ -6,8 +6,13 @@
 //   * 128x128 block scales (SMODE 1): every 128-wide K block's partial sum is
 //     scaled by sa[m, kb] * sb[n / 128, kb] and added into an fp32
 //     accumulator -- DeepSeek fp8_gemm,
-//     src/torchinferno/kernels/deepseek_v4_tilelang_definitions.py:436-485.
-// A and B are K-contiguous e4m3 (OCP float8_e4m3fn, gfx950's native FP8).
+//     src/torchinferno/kernels/deepseek_v4_tilelang_definitions.py:436-485;
+//   * MXFP4 weights (SMODE 2): B is e2m1, two per byte along K, with one E8M0
+//     scale per 32 K of a row, applied by the MFMA itself (its per-lane block
+//     scale operand); A keeps its 1x128 fp32 scales, folded per K step --
+//     DeepSeek fp4_gemm, deepseek_v4_tilelang_definitions.py:674-769.
+// A (and B outside SMODE 2) are K-contiguous e4m3 (OCP float8_e4m3fn,
+// gfx950's native FP8).
 //
 // Structure.  A workgroup owns a BM x BN output tile and walks K in steps of
 // 128 bytes.  Each step's A and B slabs (BM and BN rows of 128 B) reach LDS by
@@ -48,10 +53,24 @@ struct Mfma<32> {
   static __device__ __forceinline__ acc_t mma(i32x8 a, i32x8 b, acc_t c) {
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
   }
+  // e4m3 A x e2m1 B (blgp 4: the low four dwords of b), B block scale e8m0 eb.
+  static __device__ __forceinline__ acc_t mma4(i32x8 a, i32x8 b, acc_t c, int eb) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 4, 0, 127, 0, eb);
+  }
   // Row (within the 32x32 tile) of accumulator element e of this lane.
   static __device__ __forceinline__ int row(int e, int lane) { return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3); }
   // First of the two 16-byte chunks (of the 128-byte K step) lane reads for MFMA ks.
   static __device__ __forceinline__ int chunk(int ks, int lane) { return ks * 4 + (lane >> 5) * 2; }
+  // 16-byte chunk of a 64-byte e2m1 row (32 values) lane reads for MFMA ks;
+  // it is also the row's 32-wide scale block within the K step.
+  static __device__ __forceinline__ int chunk4(int ks, int lane) { return ks * 2 + (lane >> 5); }
+  // Against an e2m1 B the 8-bit A operand must follow the MFMA's own K order:
+  // lane group g's first 16 bytes are K [16g, 16g+16) of the 64-wide window,
+  // its last 16 bytes K [32+16g, +16), while the e2m1 operand's 16 bytes are
+  // K [32g, 32g+32).  (e4m3 x e4m3 loads both operands alike, so any order
+  // works there.)  First A chunk; the second is CHUNK_A4_HI further.
+  static __device__ __forceinline__ int chunk_a4(int ks, int lane) { return ks * 4 + (lane >> 5); }
+  static constexpr int CHUNK_A4_HI = 2;
 };
 
 template <>
@@ -62,8 +81,16 @@ struct Mfma<16> {
   static __device__ __forceinline__ acc_t mma(i32x8 a, i32x8 b, acc_t c) {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
   }
+  static __device__ __forceinline__ acc_t mma4(i32x8 a, i32x8 b, acc_t c, int eb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 4, 0, 127, 0, eb);
+  }
   static __device__ __forceinline__ int row(int e, int lane) { return 4 * (lane >> 4) + e; }
   static __device__ __forceinline__ int chunk(int, int lane) { return (lane >> 4) * 2; }
+  static __device__ __forceinline__ int chunk4(int, int lane) { return lane >> 4; }
+  // 16x16x128: lane group q holds K [16q, +16) and [64+16q, +16) of an 8-bit
+  // operand, K [32q, +32) of an e2m1 one.
+  static __device__ __forceinline__ int chunk_a4(int, int lane) { return lane >> 4; }
+  static constexpr int CHUNK_A4_HI = 4;
 };
 
 // Byte offset of 16-byte chunk c of row r in a swizzled [rows x BK bytes] slab:
@@ -72,7 +99,7 @@ struct Mfma<16> {
 // chunk cover all 64 banks.
 template <int BK>
 __device__ __forceinline__ int swz(int r, int c) {
-  constexpr int CPR = BK / 16, RP = 256 / BK;
+  constexpr int CPR = BK / 16, RP = 256 / BK;  // BK: bytes per row
   return (r * CPR + (c ^ ((r / RP) % CPR))) * 16;
 }
 
@@ -90,19 +117,25 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
   constexpr int TM = BM / WGM, TN = BN / WGN;
   constexpr int FM = TM / MF, FN = TN / MF;
   static_assert(FM >= 1 && FN >= 1 && TM % MF == 0 && TN % MF == 0, "wave tile must hold whole MFMA tiles");
-  static_assert(SMODE == 0 || 128 % TN == 0, "block scales need a wave's columns inside one 128 block");
+  static_assert(SMODE != 1 || 128 % TN == 0, "block scales need a wave's columns inside one 128 block");
   static_assert(BK == 128 || (BK == 64 && MF == 32), "16x16x128 MFMAs need 128-byte K steps");
+  static_assert(SMODE != 2 || BK == 128, "e2m1 B takes 128-wide K steps (64-byte rows)");
+  constexpr bool F4 = SMODE == 2;
+  constexpr int BROW = F4 ? BK / 2 : BK;           // B bytes per row per K step
   constexpr int KS = BK / (MF == 32 ? 64 : 128);  // MFMAs per K step
   constexpr int CPR = BK / 16;                     // 16-byte chunks per row
   constexpr int RPI = 1024 / BK;                   // rows per 1 KiB DMA
-  constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
-  // Block mode also stages the step's BM activation scales and (one 256-byte
-  // DMA) the weight scales of the tile's 128-column blocks.
-  constexpr int SA_BYTES = SMODE == 1 ? ((BM * 4 + 255) / 256) * 256 + 256 : 0;
+  constexpr int A_BYTES = BM * BK, B_BYTES = BN * BROW;
+  // Block and MXFP4 modes also stage the step's BM activation scales; block
+  // mode then the weight scales of the tile's 128-column blocks (one 256-byte
+  // DMA), MXFP4 mode the BN rows' four e8m0 bytes of the step (one dword each).
+  constexpr int SA_ROWS = SMODE >= 1 ? ((BM * 4 + 255) / 256) * 256 : 0;
+  constexpr int SB_BYTES = SMODE == 1 ? 256 : (SMODE == 2 ? ((BN * 4 + 255) / 256) * 256 : 0);
+  constexpr int SA_BYTES = SA_ROWS + SB_BYTES;
   constexpr int STAGE = A_BYTES + B_BYTES + SA_BYTES;
   constexpr int NI_AB = (A_BYTES + B_BYTES) / 1024;
-  constexpr int NI_SA = SMODE == 1 ? SA_BYTES / 256 - 1 : 0;
-  constexpr int NI = NI_AB + (SMODE == 1 ? NI_SA + 1 : 0);  // DMAs per stage, all waves
+  constexpr int NI_SA = SA_ROWS / 256;
+  constexpr int NI = NI_AB + NI_SA + SB_BYTES / 256;  // DMAs per stage, all waves
   constexpr int NI_LO = NI / W, NI_HI = (NI + W - 1) / W;
   constexpr int P = R - 1;
   static_assert(R >= 2, "ring needs two stages");
@@ -164,14 +197,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
   const uint8_t* dsrc[NI_HI];
   uint32_t dlds[NI_HI];
   bool dwide[NI_HI];
+  int dstep[NI_HI];  // source bytes per K step
 #pragma unroll
   for (int u = 0; u < NI_HI; ++u) {
     const int id = min(wave + u * W, NI - 1);
+    dstep[u] = BK;
     if (id < NI_AB) {
       const bool is_a = id < A_BYTES / 1024;
       const int j = is_a ? id : id - A_BYTES / 1024;
-      const int r = RPI * j + lane / CPR;
-      const int c = (lane % CPR) ^ ((r / (256 / BK)) % CPR);
+      const int rowb = is_a ? BK : BROW;  // slab bytes per row
+      const int cpr = rowb / 16;
+      const int r = (1024 / rowb) * j + lane / cpr;
+      const int c = (lane % cpr) ^ ((r / (256 / rowb)) % cpr);
       long row;
       if (is_a) {
         row = min(m0 + r, Mlim - 1);
@@ -179,9 +216,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
       } else {
         row = min(n0 + r, N - 1);
       }
-      dsrc[u] = (is_a ? x.a : bmat) + row * K + c * 16;
+      dsrc[u] = is_a ? x.a + row * K + c * 16 : bmat + row * (F4 ? K / 2 : K) + c * 16;
       dlds[u] = (uint32_t)((is_a ? 0 : A_BYTES) + j * 1024);
       dwide[u] = true;
+      dstep[u] = rowb;
     } else if (id < NI_AB + NI_SA) {
       const int j = id - NI_AB;
       long row = min(m0 + min(j * 64 + lane, BM - 1), Mlim - 1);
@@ -189,10 +227,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
       dsrc[u] = (const uint8_t*)(x.sa + row * KB);
       dlds[u] = (uint32_t)(A_BYTES + B_BYTES + j * 256);
       dwide[u] = false;
-    } else {
+    } else if constexpr (SMODE == 1) {
       const int nb = min(n0 / 128 + lane, (N + 127) / 128 - 1);
       dsrc[u] = (const uint8_t*)(sbmat + (long)nb * KB);
       dlds[u] = (uint32_t)(A_BYTES + B_BYTES + NI_SA * 256);
+      dwide[u] = false;
+    } else {
+      // e8m0 bytes [N, K/32]: the row's dword of K step kk sits at byte 4*kk.
+      const int j = id - NI_AB - NI_SA;
+      const int nrow = min(n0 + j * 64 + lane, N - 1);
+      dsrc[u] = (const uint8_t*)sbmat + (long)nrow * (K / 32);
+      dlds[u] = (uint32_t)(A_BYTES + B_BYTES + SA_ROWS + j * 256);
       dwide[u] = false;
     }
   }
@@ -203,7 +248,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 #pragma unroll
     for (int u = 0; u < NI_HI; ++u) {
       if (wave + u * W >= NI) break;
-      if (dwide[u]) dma16(dsrc[u] + kk * BK, base + dlds[u]);
+      if (dwide[u]) dma16(dsrc[u] + kk * dstep[u], base + dlds[u]);
       else dma4((const float*)dsrc[u] + kk * BK / 128, base + dlds[u]);
     }
   };
@@ -262,6 +307,49 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
         for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
           for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = MM::mma(af[fm], bf[fn], acc[fm][fn]);
+      }
+    } else if constexpr (SMODE == 2) {
+      const float* sS = (const float*)(st + A_BYTES + B_BYTES);
+      const uint32_t* sE = (const uint32_t*)(st + A_BYTES + B_BYTES + SA_ROWS);
+      // B fragments (16 bytes = 32 e2m1 values per lane) and their e8m0 block
+      // scales for the whole step; A is read one M tile at a time.
+      i32x8 bf[KS][FN];
+      int eb[KS][FN];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int q = MM::chunk4(ks, lane);
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const int r = brow0 + fn * MF;
+          const i32x4 lo = *(const i32x4*)(sB + swz<BROW>(r, q));
+          bf[ks][fn] = i32x8{lo[0], lo[1], lo[2], lo[3], 0, 0, 0, 0};
+          eb[ks][fn] = (int)((sE[r] >> (8 * q)) & 0xFFu);
+        }
+      }
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        i32x8 af[KS];
+        const int r = arow0 + fm * MF;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int c0 = MM::chunk_a4(ks, lane);
+          const i32x4 lo = *(const i32x4*)(sA + swz<BK>(r, c0));
+          const i32x4 hi = *(const i32x4*)(sA + swz<BK>(r, c0 + MM::CHUNK_A4_HI));
+          af[ks] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+        float srow[MM::NACC];
+#pragma unroll
+        for (int e = 0; e < MM::NACC; ++e) srow[e] = sS[wm * TM + fm * MF + MM::row(e, lane)];
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          acc_t p;
+#pragma unroll
+          for (int e = 0; e < MM::NACC; ++e) p[e] = 0.f;
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) p = MM::mma4(af[ks], bf[ks][fn], p, eb[ks][fn]);
+#pragma unroll
+          for (int e = 0; e < MM::NACC; ++e) acc[fm][fn][e] = __builtin_fmaf(p[e], srow[e], acc[fm][fn][e]);
+        }
       }
     } else {
       const float* sS = (const float*)(st + A_BYTES + B_BYTES);
@@ -380,7 +468,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 //   9  BM=256 BN=128, 8 waves 4x2 (wave 64x64),   32x32 MFMA            128     3   -- prefill
 template <int BM, int BN, int BK, int R, int SMODE>
 constexpr int cfg_lds() {
-  return R * (BM * BK + BN * BK + (SMODE == 1 ? ((BM * 4 + 255) / 256) * 256 + 256 : 0));
+  const int sa = SMODE >= 1 ? ((BM * 4 + 255) / 256) * 256 : 0;
+  const int sb = SMODE == 1 ? 256 : (SMODE == 2 ? ((BN * 4 + 255) / 256) * 256 : 0);
+  return R * (BM * BK + BN * (SMODE == 2 ? BK / 2 : BK) + sa + sb);
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, int MF, int R, int SMODE, int ODT>
@@ -396,27 +486,40 @@ void launch_cfg(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
                        lds, stream, x);
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int MF, int R>
+template <int BM, int BN, int BK, int WGM, int WGN, int MF, int R, int SMODE>
 void launch_grouped_cfg(const GemmArgs& x, int max_mtiles, hipStream_t stream) {
-  constexpr int lds = cfg_lds<BM, BN, BK, R, 1>();
+  constexpr int lds = cfg_lds<BM, BN, BK, R, SMODE>();
   dim3 grid((unsigned)(max_mtiles * x.tiles_n), 1);
-  hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, BK, WGM, WGN, MF, R, 1, 0, TI_DTYPE_BF16>), grid,
+  hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, BK, WGM, WGN, MF, R, SMODE, 0, TI_DTYPE_BF16>), grid,
                      dim3(64 * WGM * WGN), lds, stream, x);
 }
 
 template <int SMODE, int ODT>
 void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
-  switch (p.kind) {
-    case 0: launch_cfg<256, 256, 64, 2, 4, 32, 4, SMODE, ODT>(p, x, stream); break;
-    case 1: launch_cfg<256, 256, 128, 2, 4, 32, 2, SMODE, ODT>(p, x, stream); break;
-    case 2: launch_cfg<128, 128, 128, 2, 2, 32, 3, SMODE, ODT>(p, x, stream); break;
-    case 3: launch_cfg<16, 256, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
-    case 4: launch_cfg<32, 256, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
-    case 5: launch_cfg<64, 128, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
-    case 6: launch_cfg<16, 128, 128, 1, 4, 16, 6, SMODE, ODT>(p, x, stream); break;
-    case 7: launch_cfg<128, 128, 64, 2, 2, 32, 6, SMODE, ODT>(p, x, stream); break;
-    case 8: launch_cfg<256, 128, 64, 2, 2, 32, 6, SMODE, ODT>(p, x, stream); break;
-    default: launch_cfg<256, 128, 128, 4, 2, 32, 3, SMODE, ODT>(p, x, stream); break;
+  if constexpr (SMODE == 2) {
+    // MXFP4 B: the 128-wide K step kinds (the e2m1 slab is half as large, so
+    // 256x256 takes three stages).
+    switch (p.kind) {
+      case 2: launch_cfg<128, 128, 128, 2, 2, 32, 3, SMODE, ODT>(p, x, stream); break;
+      case 3: launch_cfg<16, 256, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
+      case 5: launch_cfg<64, 128, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
+      case 6: launch_cfg<16, 128, 128, 1, 4, 16, 6, SMODE, ODT>(p, x, stream); break;
+      case 9: launch_cfg<256, 128, 128, 4, 2, 32, 3, SMODE, ODT>(p, x, stream); break;
+      default: launch_cfg<256, 256, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
+    }
+  } else {
+    switch (p.kind) {
+      case 0: launch_cfg<256, 256, 64, 2, 4, 32, 4, SMODE, ODT>(p, x, stream); break;
+      case 1: launch_cfg<256, 256, 128, 2, 4, 32, 2, SMODE, ODT>(p, x, stream); break;
+      case 2: launch_cfg<128, 128, 128, 2, 2, 32, 3, SMODE, ODT>(p, x, stream); break;
+      case 3: launch_cfg<16, 256, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
+      case 4: launch_cfg<32, 256, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
+      case 5: launch_cfg<64, 128, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
+      case 6: launch_cfg<16, 128, 128, 1, 4, 16, 6, SMODE, ODT>(p, x, stream); break;
+      case 7: launch_cfg<128, 128, 64, 2, 2, 32, 6, SMODE, ODT>(p, x, stream); break;
+      case 8: launch_cfg<256, 128, 64, 2, 2, 32, 6, SMODE, ODT>(p, x, stream); break;
+      default: launch_cfg<256, 128, 128, 4, 2, 32, 3, SMODE, ODT>(p, x, stream); break;
+    }
   }
 }
 
@@ -453,7 +556,7 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
     splits = tiles(64, 128) >= 128 ? 1 : 2;
   } else if (tiles(256, 256) >= 256) {
     p.kind = 1;
-  } else if (tiles(256, 128) >= (smode == 1 ? 128 : 256)) {
+  } else if (tiles(256, 128) >= (smode >= 1 ? 128 : 256)) {
     p.kind = 9;
   } else {
     p.kind = 2;
@@ -461,6 +564,7 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   }
   p.kind = env_int("TI_ROCM_FP8_KIND", p.kind);
   if (p.kind < 0 || p.kind >= kNumKinds) p.kind = 1;
+  if (smode == 2 && (p.kind == 0 || p.kind == 4 || p.kind == 7 || p.kind == 8)) p.kind = 1;  // not built for e2m1
   p.group_m = env_int("TI_ROCM_FP8_GROUP_M", 4);
   if (p.group_m < 1) p.group_m = 1;
   p.tiles_m = cdiv(M, kBM[p.kind]);
@@ -474,13 +578,19 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
 int grouped_bm(int kind) { return kBM[kind]; }
 int grouped_bn(int kind) { return kBN[kind]; }
 
-void launch_gemm_grouped(int kind, const GemmArgs& x, int max_mtiles, hipStream_t stream) {
+template <int SMODE>
+void launch_grouped_smode(int kind, const GemmArgs& x, int max_mtiles, hipStream_t stream) {
   switch (kind) {
-    case 2: launch_grouped_cfg<128, 128, 128, 2, 2, 32, 3>(x, max_mtiles, stream); break;
-    case 5: launch_grouped_cfg<64, 128, 128, 1, 4, 16, 4>(x, max_mtiles, stream); break;
-    case 9: launch_grouped_cfg<256, 128, 128, 4, 2, 32, 3>(x, max_mtiles, stream); break;
-    default: launch_grouped_cfg<16, 128, 128, 1, 4, 16, 6>(x, max_mtiles, stream); break;
+    case 2: launch_grouped_cfg<128, 128, 128, 2, 2, 32, 3, SMODE>(x, max_mtiles, stream); break;
+    case 5: launch_grouped_cfg<64, 128, 128, 1, 4, 16, 4, SMODE>(x, max_mtiles, stream); break;
+    case 9: launch_grouped_cfg<256, 128, 128, 4, 2, 32, 3, SMODE>(x, max_mtiles, stream); break;
+    default: launch_grouped_cfg<16, 128, 128, 1, 4, 16, 6, SMODE>(x, max_mtiles, stream); break;
   }
+}
+
+void launch_gemm_grouped(int kind, int smode, const GemmArgs& x, int max_mtiles, hipStream_t stream) {
+  if (smode == 2) launch_grouped_smode<2>(kind, x, max_mtiles, stream);
+  else launch_grouped_smode<1>(kind, x, max_mtiles, stream);
 }
 
 size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
@@ -498,6 +608,9 @@ void launch_gemm(const GemmPlan& p, int smode, int odt, const GemmArgs& x, hipSt
   if (smode == 0) {
     if (odt == TI_DTYPE_F16) launch_kind<0, TI_DTYPE_F16>(p, x, stream);
     else launch_kind<0, TI_DTYPE_BF16>(p, x, stream);
+  } else if (smode == 2) {
+    if (odt == TI_DTYPE_F16) launch_kind<2, TI_DTYPE_F16>(p, x, stream);
+    else launch_kind<2, TI_DTYPE_BF16>(p, x, stream);
   } else {
     if (odt == TI_DTYPE_F16) launch_kind<1, TI_DTYPE_F16>(p, x, stream);
     else launch_kind<1, TI_DTYPE_BF16>(p, x, stream);
@@ -578,4 +691,11 @@ extern "C" int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, const u
                                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
   return gemm_common("ti_fp8_gemm_block", 1, a, a_scale, 0, b, b_scale, 0, out, out_dtype, M, N, K, workspace,
                      workspace_bytes, stream);
+}
+
+extern "C" int ti_fp4_gemm(const uint8_t* a, const float* a_scale, const uint8_t* b, const uint8_t* b_scale,
+                           void* out, int out_dtype, int M, int N, int K, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream) {
+  return gemm_common("ti_fp4_gemm", 2, a, a_scale, 0, b, (const float*)b_scale, 0, out, out_dtype, M, N, K,
+                     workspace, workspace_bytes, stream);
 }

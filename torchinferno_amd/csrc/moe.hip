@@ -324,27 +324,31 @@ extern "C" size_t ti_fp8_moe_workspace_bytes(int T, int k, int E, int H, int I) 
   return carve(nullptr, T, k, H, I, p).bytes;
 }
 
-extern "C" int ti_fp8_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids, int T, int k,
-                          const uint8_t* w13, const float* s13, const uint8_t* w2, const float* s2, int E, int H,
-                          int I, float clamp_limit, void* out, void* workspace, size_t workspace_bytes,
-                          hipStream_t stream) {
-  TI_CHECK_ARG(hidden && topk_weights && topk_ids && w13 && s13 && w2 && s2 && out, "ti_fp8_moe: null pointer");
+// Routed experts, shared by the block-FP8 (smode 1: e4m3 weights, 128x128
+// fp32 scales) and MXFP4 (smode 2: e2m1 weights two per byte, e8m0 scale per
+// 32 K) weight formats; activations are 1x128 block FP8 in both.
+static int moe_run(const char* name, int smode, const void* hidden, const float* topk_weights,
+                   const int32_t* topk_ids, int T, int k, const uint8_t* w13, const void* s13, const uint8_t* w2,
+                   const void* s2, int E, int H, int I, float clamp_limit, void* out, void* workspace,
+                   size_t workspace_bytes, hipStream_t stream) {
+  TI_CHECK_ARG(hidden && topk_weights && topk_ids && w13 && s13 && w2 && s2 && out, "%s: null pointer", name);
   TI_CHECK_SHAPE(moe_shape_ok(T, k, E, H, I),
-                 "ti_fp8_moe: need H %% 128 == 0, I %% 128 == 0, 1 <= k <= 16, E <= 1024 (T=%d k=%d E=%d H=%d I=%d)",
-                 T, k, E, H, I);
+                 "%s: need H %% 128 == 0, I %% 128 == 0, 1 <= k <= 16, E <= 1024 (T=%d k=%d E=%d H=%d I=%d)",
+                 name, T, k, E, H, I);
   TI_CHECK_ARG(((uintptr_t)hidden & 15) == 0 && ((uintptr_t)w13 & 15) == 0 && ((uintptr_t)w2 & 15) == 0 &&
-                   ((uintptr_t)out & 3) == 0,
-               "ti_fp8_moe: hidden, w13, w2 must be 16-byte and out 4-byte aligned");
+                   ((uintptr_t)out & 3) == 0 && ((uintptr_t)s13 & 3) == 0 && ((uintptr_t)s2 & 3) == 0,
+               "%s: hidden, w13, w2 must be 16-byte and out, scales 4-byte aligned", name);
   if (T == 0) return TI_OK;
   Plan p = make_plan(T, k, E);
   Ws w = carve(nullptr, T, k, H, I, p);
   if (!workspace || workspace_bytes < w.bytes) {
-    set_error("ti_fp8_moe: workspace of %zu bytes required (got %zu)", w.bytes, workspace_bytes);
+    set_error("%s: workspace of %zu bytes required (got %zu)", name, w.bytes, workspace_bytes);
     return TI_ERR_WORKSPACE;
   }
-  TI_CHECK_ARG(((uintptr_t)workspace & 255) == 0, "ti_fp8_moe: workspace must be 256-byte aligned");
+  TI_CHECK_ARG(((uintptr_t)workspace & 255) == 0, "%s: workspace must be 256-byte aligned", name);
   w = carve((uint8_t*)workspace, T, k, H, I, p);
   const long R = (long)T * k;
+  const bool f4 = smode == 2;
 
   // 1. hidden -> e4m3 1x128
   int st = ti_fp8_quant_block(hidden, TI_DTYPE_BF16, T, H, 128, 0, w.xq, w.xs, stream);
@@ -353,40 +357,56 @@ extern "C" int ti_fp8_moe(const void* hidden, const float* topk_weights, const i
   hipLaunchKernelGGL(align_kernel, dim3(1), dim3(kAlignThreads), 0, stream, (const int*)topk_ids, (int)R, E, p.bm,
                      w.pos_of_route, w.tok_of_pos, w.route_of_pos, k, w.tile_expert, w.tile_row0, w.tile_rows,
                      w.num_tiles);
-  TI_CHECK_LAUNCH("ti_fp8_moe(align)");
+  TI_CHECK_LAUNCH("moe(align)");
   // 3. grouped w13: [R, 2I] = xq[tok] . w13[e]^T
   fp8::GemmArgs g{};
-  g.a = w.xq; g.sa = w.xs; g.b = w13; g.sb = s13;
+  g.a = w.xq; g.sa = w.xs; g.b = w13; g.sb = (const float*)s13;
   g.row_index = w.tok_of_pos;
   g.out = w.out1;
   g.M = (int)R; g.N = 2 * I; g.K = H;
   g.splits = 1; g.tiles_m = 0; g.tiles_n = cdiv(2 * I, fp8::grouped_bn(p.kind)); g.group_m = 1;
   g.grouped = 1; g.tile_expert = w.tile_expert; g.tile_row0 = w.tile_row0; g.tile_rows = w.tile_rows;
   g.num_mtiles = w.num_tiles;
-  g.b_expert_stride = (long)2 * I * H;
-  g.sb_expert_stride = (long)cdiv(2 * I, 128) * (H / 128);
-  fp8::launch_gemm_grouped(p.kind, g, p.max_tiles, stream);
-  TI_CHECK_LAUNCH("ti_fp8_moe(w13)");
+  g.b_expert_stride = f4 ? (long)I * H : (long)2 * I * H;
+  g.sb_expert_stride = f4 ? (long)2 * I * H / 128 : (long)cdiv(2 * I, 128) * (H / 128);
+  fp8::launch_gemm_grouped(p.kind, smode, g, p.max_tiles, stream);
+  TI_CHECK_LAUNCH("moe(w13)");
   // 4. swiglu x route weight -> 1x128 quant
   const long items = R * (I / 128);
   hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, w.out1, I,
                      topk_weights, w.route_of_pos, w.num_tiles, w.tile_row0, w.tile_rows, R, clamp_limit, w.hq,
                      w.hs);
-  TI_CHECK_LAUNCH("ti_fp8_moe(swiglu)");
+  TI_CHECK_LAUNCH("moe(swiglu)");
   // 5. grouped w2: [R, H] = hq . w2[e]^T
   fp8::GemmArgs g2 = g;
-  g2.a = w.hq; g2.sa = w.hs; g2.b = w2; g2.sb = s2;
+  g2.a = w.hq; g2.sa = w.hs; g2.b = w2; g2.sb = (const float*)s2;
   g2.row_index = nullptr;
   g2.out = w.out2;
   g2.N = H; g2.K = I;
   g2.tiles_n = cdiv(H, fp8::grouped_bn(p.kind));
-  g2.b_expert_stride = (long)H * I;
-  g2.sb_expert_stride = (long)cdiv(H, 128) * (I / 128);
-  fp8::launch_gemm_grouped(p.kind, g2, p.max_tiles, stream);
-  TI_CHECK_LAUNCH("ti_fp8_moe(w2)");
+  g2.b_expert_stride = f4 ? (long)H * I / 2 : (long)H * I;
+  g2.sb_expert_stride = f4 ? (long)H * I / 128 : (long)cdiv(H, 128) * (I / 128);
+  fp8::launch_gemm_grouped(p.kind, smode, g2, p.max_tiles, stream);
+  TI_CHECK_LAUNCH("moe(w2)");
   // 6. combine
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)T), dim3(256), 0, stream, w.out2, H, (const int*)topk_ids,
                      w.pos_of_route, k, (uint16_t*)out);
-  TI_CHECK_LAUNCH("ti_fp8_moe(combine)");
+  TI_CHECK_LAUNCH("moe(combine)");
   return TI_OK;
+}
+
+extern "C" int ti_fp8_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids, int T, int k,
+                          const uint8_t* w13, const float* s13, const uint8_t* w2, const float* s2, int E, int H,
+                          int I, float clamp_limit, void* out, void* workspace, size_t workspace_bytes,
+                          hipStream_t stream) {
+  return moe_run("ti_fp8_moe", 1, hidden, topk_weights, topk_ids, T, k, w13, s13, w2, s2, E, H, I, clamp_limit, out,
+                 workspace, workspace_bytes, stream);
+}
+
+extern "C" int ti_fp4_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids, int T, int k,
+                          const uint8_t* w13, const uint8_t* s13, const uint8_t* w2, const uint8_t* s2, int E, int H,
+                          int I, float clamp_limit, void* out, void* workspace, size_t workspace_bytes,
+                          hipStream_t stream) {
+  return moe_run("ti_fp4_moe", 2, hidden, topk_weights, topk_ids, T, k, w13, s13, w2, s2, E, H, I, clamp_limit, out,
+                 workspace, workspace_bytes, stream);
 }

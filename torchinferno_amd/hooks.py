@@ -282,32 +282,35 @@ def patch_fused_producers(module: types.ModuleType) -> Callable[[], None]:
 
 
 def deepseek_linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
-    """DSv4 ``linear`` (tensor_parallel.py:195-207): e4m3 weights (with ``.scale``,
-    128x128 blocks) run act_quant + the block-FP8 GEMM here; other dtypes keep
-    ``F.linear`` (MXFP4 experts are not covered by this package)."""
+    """DSv4 ``linear`` (tensor_parallel.py:195-207): e4m3 weights (``.scale``
+    per 128x128 block) and MXFP4 weights (``float4_e2m1fn_x2``, ``.scale`` one
+    E8M0 per 32 K) run act_quant + the block-FP8 / FP4 GEMM here; other dtypes
+    keep ``F.linear``."""
     from .kernels import block_fp8
 
     assert bias is None
-    if weight.dtype == torch.float8_e4m3fn:
+    if weight.dtype in (torch.float8_e4m3fn, torch.float4_e2m1fn_x2):
         return block_fp8.linear(x, weight, weight.scale)
-    if weight.dtype == getattr(torch, "float4_e2m1fn_x2", None):
-        raise NotImplementedError("MXFP4 weights are not supported by torchinferno_amd")
     return torch.nn.functional.linear(x, weight)
 
 
 def prepare_fused_fp8_experts(moe_module) -> bool:
-    """Stack a DSv4 ``MoE``'s local block-FP8 experts into the grouped layout
-    (the role of ``MoE.prepare_fused_experts``, tensor_parallel.py:826-858)."""
+    """Stack a DSv4 ``MoE``'s local block-FP8 or MXFP4 experts into the grouped
+    layout (the role of ``MoE.prepare_fused_experts``, tensor_parallel.py:826-858)."""
     from .kernels import moe as _moe
 
     if getattr(moe_module, "_ti_fused_experts", None) is not None:
         return True
     start, end = moe_module.experts_start_idx, moe_module.experts_end_idx
     local = [moe_module.experts[i] for i in range(start, end)]
-    if not local or local[0] is None or local[0].w1.weight.dtype != torch.float8_e4m3fn:
+    if not local or local[0] is None:
+        return False
+    dtype = local[0].w1.weight.dtype
+    if dtype not in (torch.float8_e4m3fn, torch.float4_e2m1fn_x2):
         return False
     st = torch.stack
-    moe_module._ti_fused_experts = _moe.prepare_fp8_experts(
+    prepare = _moe.prepare_fp8_experts if dtype == torch.float8_e4m3fn else _moe.prepare_mxfp4_experts
+    moe_module._ti_fused_experts = prepare(
         st([e.w1.weight for e in local]), st([e.w3.weight for e in local]), st([e.w2.weight for e in local]),
         st([e.w1.scale for e in local]), st([e.w3.scale for e in local]), st([e.w2.scale for e in local]),
         expert_start=start, global_num_experts=moe_module.n_routed_experts)
@@ -325,8 +328,9 @@ def moe_forward(self, x: Tensor, input_ids: Tensor) -> Tensor:
     weights, indices = self.gate(x, input_ids.flatten())
     fused = getattr(self, "_ti_fused_experts", None)
     if fused is not None:
-        y = _moe.fused_fp8_moe(x.contiguous(), weights.float().contiguous(), indices.int().contiguous(), fused,
-                               clamp_limit=float(getattr(self.shared_experts, "swiglu_limit", 0.0) or 0.0))
+        run = _moe.fused_mxfp4_moe if isinstance(fused, _moe.PreparedMxfp4Experts) else _moe.fused_fp8_moe
+        y = run(x.contiguous(), weights.float().contiguous(), indices.int().contiguous(), fused,
+                clamp_limit=float(getattr(self.shared_experts, "swiglu_limit", 0.0) or 0.0))
         y = y.float()
     else:
         y = torch.zeros_like(x, dtype=torch.float32)

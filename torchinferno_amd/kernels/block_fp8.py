@@ -5,8 +5,11 @@
 ``act_quant(x)``: 1x128 activation quant, ``s = max(amax, 1e-4) / 448`` (or the
 power-of-two ceiling when ``scale_fmt`` is set), ``y = clamp(x / s, +-448)``.
 ``fp8_gemm(a, a_s, b, b_s)``: ``C = sum_kb (a . b^T)_kb * a_s[:, kb] * b_s[n/128, kb]``,
-bf16 out.  Both run libti_quant.so's gfx950 kernels.  Scales are fp32; the
-reference's ``float8_e8m0fnu`` scale storage is not supported (ValueError).
+bf16 out.  ``fp4_gemm(a, a_s, b, b_s)``: FP8 activations x MXFP4 weights
+(deepseek_v4_tilelang_definitions.py:674-769): ``b`` e2m1 ``[N, K/2]``, ``b_s`` one
+E8M0 scale per 32 K (``float8_e8m0fnu``, or fp32 powers of two).  All run
+libti_quant.so's gfx950 kernels.  Activation scales are fp32; the reference's
+``float8_e8m0fnu`` activation-scale storage is not supported (ValueError).
 """
 from __future__ import annotations
 
@@ -88,8 +91,64 @@ def fp8_gemm(
     return out
 
 
+FP4 = torch.float4_e2m1fn_x2
+
+
+def e8m0_bytes(scale: Tensor) -> Tensor:
+    """MXFP4 weight scales as E8M0 bytes: ``float8_e8m0fnu`` (or uint8) storage as
+    is; fp32 only when every value is an exact power of two, else ValueError."""
+    if scale.dtype == torch.float8_e8m0fnu:
+        return scale.contiguous().view(torch.uint8)
+    if scale.dtype == torch.uint8:
+        return scale.contiguous()
+    if scale.dtype != torch.float32:
+        raise ValueError("MXFP4 scales must be float8_e8m0fnu, uint8 E8M0 bytes or fp32 powers of two")
+    b = scale.to(torch.float8_e8m0fnu)
+    if not torch.equal(b.float(), scale):
+        raise ValueError("fp32 MXFP4 scales must be exact powers of two")
+    return b.contiguous().view(torch.uint8)
+
+
+def fp4_gemm(
+    a: Tensor,
+    a_s: Tensor,
+    b: Tensor,
+    b_s: Tensor,
+    scale_dtype: torch.dtype = torch.float32,
+) -> Tensor:
+    """``C[M,N] = A_fp8[M,K] @ B_fp4[N,K]^T`` (bf16 out): ``a`` e4m3 ``[..., K]`` with
+    fp32 1x128 scales ``a_s [..., K/128]``; ``b`` ``float4_e2m1fn_x2`` (or uint8)
+    ``[N, K/2]``; ``b_s`` per-32 E8M0 scales ``[N, K/32]``."""
+    if not all(t.is_contiguous() for t in (a, a_s, b, b_s)):
+        raise ValueError("FP4 GEMM inputs and scales must be contiguous")
+    _check_scale_dtype(scale_dtype)
+    if a.dtype != FP8_E4M3 or b.dtype not in (FP4, torch.uint8):
+        raise ValueError("FP4 GEMM operands must be float8_e4m3fn activations and float4_e2m1fn_x2 weights")
+    if a_s.dtype != torch.float32:
+        raise ValueError("FP4 GEMM activation scales must be fp32")
+    _lib.require_device(a, a_s, b, b_s)
+    k = a.size(-1)
+    m = a.numel() // k
+    n = b.size(0)
+    if b.ndim != 2 or b.size(1) * 2 != k:
+        raise ValueError("FP4 GEMM weight must be [N, K/2] packed e2m1 with the activation's K")
+    if k % BLOCK:
+        raise ValueError("FP4 GEMM needs K divisible by 128")
+    eb = e8m0_bytes(b_s)
+    if a_s.numel() != m * (k // BLOCK) or tuple(eb.shape) != (n, k // 32):
+        raise ValueError("FP4 GEMM scales must be a_s [M, K/128] and b_s [N, K/32]")
+    out = torch.empty((*a.shape[:-1], n), dtype=torch.bfloat16, device=a.device)
+    ws, ws_bytes = _ws_args(a.device, m, n, k, 2)
+    _lib.call("ti_fp4_gemm", a.data_ptr(), a_s.data_ptr(), b.data_ptr(), eb.data_ptr(), out.data_ptr(),
+              _lib.TI_DTYPE_BF16, m, n, k, ws, ws_bytes, _lib.stream_of(a))
+    return out
+
+
 def linear(x: Tensor, weight: Tensor, weight_scale: Tensor) -> Tensor:
-    """DeepSeek ``linear`` for an e4m3 weight (src/torchinferno/models/deepseek_v4/
-    tensor_parallel.py:195-207): ``act_quant`` then ``fp8_gemm``, bf16 out."""
+    """DeepSeek ``linear`` for an e4m3 or MXFP4 weight (src/torchinferno/models/
+    deepseek_v4/tensor_parallel.py:195-207): ``act_quant`` then ``fp8_gemm`` /
+    ``fp4_gemm``, bf16 out."""
     xq, xs = act_quant(x)
+    if weight.dtype == FP4:
+        return fp4_gemm(xq, xs, weight, weight_scale)
     return fp8_gemm(xq, xs, weight, weight_scale)

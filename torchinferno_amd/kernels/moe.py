@@ -1,7 +1,12 @@
-"""Routed FP8 block-scaled MoE on MI355X -- drop-in for the reference's grouped expert
-path (src/torchinferno/kernels/deepseek_v4_marlin.py: ``prepare_mxfp4_experts``
-:194-264, ``fused_mxfp4_moe`` :311-411) with DeepSeek-V3-style FP8 experts
-(128x128 block scales) instead of MXFP4.
+"""Routed MoE on MI355X -- drop-in for the reference's grouped expert path
+(src/torchinferno/kernels/deepseek_v4_marlin.py: ``prepare_mxfp4_experts``
+:194-264, ``fused_mxfp4_moe`` :311-411), for DeepSeek-V3-style FP8 experts
+(128x128 block scales: ``prepare_fp8_experts`` / ``fused_fp8_moe``) and for DSv4
+MXFP4 experts (e2m1 weights, E8M0 scale per 32: ``prepare_mxfp4_experts`` /
+``fused_mxfp4_moe``, same names and arguments as the reference).  Both run 1x128
+FP8 activations through gfx950 block-scaled MFMAs; for MXFP4 that is the
+arithmetic of the reference's TileLang expert path (act_quant + fp4_gemm), not
+of its bf16-activation Marlin kernel.
 
 ``route_topk`` is the softmax gate (DSv4 ``Gate.forward``,
 src/torchinferno/models/deepseek_v4/tensor_parallel.py:760-780; V3.2
@@ -20,6 +25,7 @@ import torch
 from torch import Tensor
 
 from .. import _lib
+from .block_fp8 import FP4, e8m0_bytes
 from .fp8 import FP8_E4M3
 
 _ws_lock = threading.Lock()
@@ -72,6 +78,59 @@ def prepare_fp8_experts(w1: Tensor, w3: Tensor, w2: Tensor, w1_scale: Tensor, w3
     )
 
 
+@dataclass(frozen=True)
+class PreparedMxfp4Experts:
+    """One GPU's MXFP4 experts in the kernel layout: ``w13 = [w1; w3]`` per expert."""
+
+    w13: Tensor        # e2m1 x2 (uint8) [E, 2I, H/2]
+    w13_scale: Tensor  # E8M0 bytes [E, 2I, H/32]
+    w2: Tensor         # e2m1 x2 (uint8) [E, H, I/2]
+    w2_scale: Tensor   # E8M0 bytes [E, H, I/32]
+    expert_map: Tensor  # int32 [global experts] -> local index or -1
+    global_num_experts: int
+    hidden_size: int
+    intermediate_size: int
+
+
+def prepare_mxfp4_experts(w1: Tensor, w3: Tensor, w2: Tensor, w1_scale: Tensor, w3_scale: Tensor,
+                          w2_scale: Tensor, *, expert_start: int = 0,
+                          global_num_experts: int | None = None) -> PreparedMxfp4Experts:
+    """Stack one GPU's native MXFP4 experts (deepseek_v4_marlin.py:194-264, same
+    arguments): ``w1``/``w3`` ``[E, I, H/2]`` and ``w2`` ``[E, H, I/2]``
+    ``float4_e2m1fn_x2``; scales one E8M0 per 32 K (``[E, I, H/32]``,
+    ``[E, H, I/32]``).  No repacking: the kernels read the checkpoint layout."""
+    if w1.ndim != 3 or w3.ndim != 3 or w2.ndim != 3:
+        raise ValueError("expert weights must be stacked [experts, output, packed-K]")
+    if tuple(w1.shape) != tuple(w3.shape):
+        raise ValueError("w1 and w3 expert shapes must match")
+    e, inter, half_h = w1.shape
+    hidden = half_h * 2
+    if tuple(w2.shape) != (e, hidden, inter // 2):
+        raise ValueError("w2 expert shape does not match w1/w3")
+    if any(t.dtype not in (FP4, torch.uint8) for t in (w1, w3, w2)):
+        raise ValueError("expert weights must be float4_e2m1fn_x2")
+    if hidden % 128 or inter % 128:
+        raise ValueError("hidden and intermediate sizes must be multiples of 128")
+    s1, s3, s2 = (e8m0_bytes(t) for t in (w1_scale, w3_scale, w2_scale))
+    if tuple(s1.shape) != (e, inter, hidden // 32) or tuple(s3.shape) != tuple(s1.shape) \
+            or tuple(s2.shape) != (e, hidden, inter // 32):
+        raise ValueError("MXFP4 scales must be one E8M0 per 32 K of each weight row")
+    global_num_experts = e if global_num_experts is None else global_num_experts
+    expert_map = torch.full((global_num_experts,), -1, dtype=torch.int32, device=w1.device)
+    expert_map[expert_start:expert_start + e] = torch.arange(e, dtype=torch.int32, device=w1.device)
+    u8 = lambda t: t.contiguous().view(torch.uint8)  # noqa: E731
+    return PreparedMxfp4Experts(
+        w13=torch.cat((u8(w1), u8(w3)), dim=1).contiguous(),
+        w13_scale=torch.cat((s1, s3), dim=1).contiguous(),
+        w2=u8(w2),
+        w2_scale=s2.contiguous(),
+        expert_map=expert_map,
+        global_num_experts=global_num_experts,
+        hidden_size=hidden,
+        intermediate_size=inter,
+    )
+
+
 def route_topk(logits: Tensor, k: int, *, renormalize: bool = True,
                route_scale: float = 1.0) -> tuple[Tensor, Tensor]:
     """Softmax top-k router: (weights fp32 [T,k], ids int32 [T,k]), descending."""
@@ -97,11 +156,8 @@ def _workspace(device: torch.device, nbytes: int) -> Tensor:
         return ws
 
 
-def fused_fp8_moe(hidden_states: Tensor, topk_weights: Tensor, topk_ids: Tensor,
-                  experts: PreparedFp8Experts, *, clamp_limit: float = 0.0) -> Tensor:
-    """Grouped routed experts for one GPU (signature of fused_mxfp4_moe,
-    deepseek_v4_marlin.py:311-318).  ``topk_ids`` are global expert ids; routes to
-    experts this GPU does not hold contribute nothing.  Returns bf16 [T, H]."""
+def _routed(entry: str, hidden_states: Tensor, topk_weights: Tensor, topk_ids: Tensor, experts,
+            clamp_limit: float) -> Tensor:
     if hidden_states.ndim != 2 or not hidden_states.is_contiguous():
         raise ValueError("hidden_states must be a contiguous matrix")
     if hidden_states.dtype != torch.bfloat16:
@@ -124,11 +180,26 @@ def fused_fp8_moe(hidden_states: Tensor, topk_weights: Tensor, topk_ids: Tensor,
     ws = _workspace(hidden_states.device, need)
     base = ws.data_ptr()
     aligned = (base + 255) & ~255
-    _lib.call("ti_fp8_moe", hidden_states.data_ptr(), weights.data_ptr(), local_ids.data_ptr(), tokens, k,
+    _lib.call(entry, hidden_states.data_ptr(), weights.data_ptr(), local_ids.data_ptr(), tokens, k,
               experts.w13.data_ptr(), experts.w13_scale.data_ptr(), experts.w2.data_ptr(),
               experts.w2_scale.data_ptr(), e_local, hidden, inter, float(clamp_limit), out.data_ptr(),
               aligned, ws.numel() - (aligned - base), _lib.stream_of(hidden_states))
     return out
+
+
+def fused_fp8_moe(hidden_states: Tensor, topk_weights: Tensor, topk_ids: Tensor,
+                  experts: PreparedFp8Experts, *, clamp_limit: float = 0.0) -> Tensor:
+    """Grouped routed experts for one GPU (signature of fused_mxfp4_moe,
+    deepseek_v4_marlin.py:311-318).  ``topk_ids`` are global expert ids; routes to
+    experts this GPU does not hold contribute nothing.  Returns bf16 [T, H]."""
+    return _routed("ti_fp8_moe", hidden_states, topk_weights, topk_ids, experts, clamp_limit)
+
+
+def fused_mxfp4_moe(hidden_states: Tensor, topk_weights: Tensor, topk_ids: Tensor,
+                    experts: PreparedMxfp4Experts, *, clamp_limit: float = 0.0) -> Tensor:
+    """MXFP4 routed experts (deepseek_v4_marlin.py:311-411, same arguments and
+    [T, H] bf16 result); see ``fused_fp8_moe`` for routing semantics."""
+    return _routed("ti_fp4_moe", hidden_states, topk_weights, topk_ids, experts, clamp_limit)
 
 
 def moe_forward(hidden_states: Tensor, router_logits: Tensor, experts: PreparedFp8Experts, k: int, *,
