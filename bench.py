@@ -14,8 +14,9 @@ algorithmic bytes (or flops) over its average duration, measured with HIP
 events on the stream the kernel runs on.  ``points`` lists every BASELINE
 config measured the same way: config 0 (int4 fp16), config 2 (FP8 per-token x
 per-channel, Llama-3-70B, plus its fused add+RMSNorm / SwiGLU -> FP8
-activation producers), config 3 (DeepSeek 128x128 block FP8) and config 4
-(routed FP8 MoE, 256 experts, top-8, router included).  ``cpu_baseline`` times
+activation producers), config 3 (DeepSeek 128x128 block FP8, and the same
+shapes with MXFP4 weights) and config 4 (routed FP8 MoE, 256 experts, top-8,
+router included, and the same experts in MXFP4).  ``cpu_baseline`` times
 the CPU oracle (dequantize-then-matmul, oracle/int4.py) on one gate_up M=32 GEMM.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only int4|fp8|moe]
@@ -212,13 +213,20 @@ def fp8_points(dev, stream):
     L = _lib.lib()
     ws = torch.zeros(64 << 20, dtype=torch.int32, device=dev)
     recs = []
-    for mode, shapes, ms in ((0, FP8_SHAPES, FP8_MS), (1, BLOCK_SHAPES, BLOCK_MS)):
+    for mode, shapes, ms in ((0, FP8_SHAPES, FP8_MS), (1, BLOCK_SHAPES, BLOCK_MS), (2, BLOCK_SHAPES, BLOCK_MS)):
         for sname, (k, n) in shapes.items():
-            ncopy = max(2, -(-ROTATE_BYTES // (n * k)))
-            bq = [torch.randint(-120, 120, (n, k), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
-                  for _ in range(ncopy)]
-            bs = [torch.rand((n,) if mode == 0 else (-(-n // 128), k // 128), device=dev) * 1e-3 + 1e-4
-                  for _ in range(ncopy)]
+            wbytes_n = n * k // 2 if mode == 2 else n * k
+            ncopy = max(2, -(-ROTATE_BYTES // wbytes_n))
+            if mode == 2:  # MXFP4: e2m1 pairs, e8m0 scale per 32 K
+                bq = [torch.randint(0, 256, (n, k // 2), device=dev, dtype=torch.uint8) for _ in range(ncopy)]
+                from torchinferno_amd.kernels.block_fp8 import fp4_scale_stepmajor
+                bs = [fp4_scale_stepmajor(torch.randint(118, 130, (n, k // 32), device=dev, dtype=torch.uint8))
+                      for _ in range(ncopy)]
+            else:
+                bq = [torch.randint(-120, 120, (n, k), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
+                      for _ in range(ncopy)]
+                bs = [torch.rand((n,) if mode == 0 else (-(-n // 128), k // 128), device=dev) * 1e-3 + 1e-4
+                      for _ in range(ncopy)]
             for m in ms:
                 a = torch.randint(-120, 120, (m, k), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
                 asc = torch.rand((m,) if mode == 0 else (m, k // 128), device=dev) * 0.01 + 1e-3
@@ -231,6 +239,9 @@ def fp8_points(dev, stream):
                     if mode == 0:
                         r = L.ti_fp8_gemm_rowcol(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(),
                                                  1, out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
+                    elif mode == 2:
+                        r = L.ti_fp4_gemm(a.data_ptr(), asc.data_ptr(), bq[j].data_ptr(), bs[j].data_ptr(), 1,
+                                          out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
                     else:
                         r = L.ti_fp8_gemm_block(a.data_ptr(), asc.data_ptr(), bq[j].data_ptr(), bs[j].data_ptr(),
                                                 out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
@@ -240,12 +251,13 @@ def fp8_points(dev, stream):
                 timed_burst([launch], 3, stream)
                 t = timed_burst([launch], reps, stream) / reps * 1e-3
                 flops = 2 * m * n * k
-                scale_bytes = n * 4 if mode == 0 else (-(-n // 128)) * (k // 128) * 4
-                algo = n * k + scale_bytes + m * k + m * n * 2
+                scale_bytes = (n * 4 if mode == 0 else (-(-n // 128)) * (k // 128) * 4 if mode == 1
+                               else n * (k // 32))
+                algo = wbytes_n + scale_bytes + m * k + m * n * 2
                 bound = "mfma" if flops / algo > FP8_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
-                cfg = "config2" if mode == 0 else "config3"
-                recs.append(point_record(f"{cfg} fp8 {'rowcol' if mode == 0 else 'block'} {sname} M={m} K={k} N={n}",
-                                         t, algo, flops, bound, FP8_PEAK_TFLOPS))
+                label = {0: "config2 fp8 rowcol", 1: "config3 fp8 block", 2: "config3-shape mxfp4"}[mode]
+                recs.append(point_record(f"{label} {sname} M={m} K={k} N={n}", t, algo, flops, bound,
+                                         FP8_PEAK_TFLOPS))
                 log(recs[-1])
             del bq, bs
             torch.cuda.empty_cache()
@@ -312,6 +324,28 @@ def moe_points(dev, stream):
     s2 = torch.rand((e, h // 128, inter // 128), device=dev) * 1e-3 + 1e-4
     recs = []
     per_expert = 2 * inter * h + h * inter + (s13[0].numel() + s2[0].numel()) * 4
+    recs += _moe_sweep(L, dev, "config4 fp8 moe", "ti_fp8_moe", w13, s13, w2, s2, e, h, inter, k, per_expert)
+    del w13, w2, s13, s2
+    torch.cuda.empty_cache()
+    # The same routed experts with MXFP4 weights (e2m1 pairs, e8m0 per 32 K).
+    w13 = torch.randint(0, 256, (e, 2 * inter, h // 2), device=dev, dtype=torch.uint8)
+    w2 = torch.randint(0, 256, (e, h, inter // 2), device=dev, dtype=torch.uint8)
+    from torchinferno_amd.kernels.block_fp8 import fp4_scale_stepmajor
+    s13 = fp4_scale_stepmajor(torch.randint(118, 124, (e, 2 * inter, h // 32), device=dev, dtype=torch.uint8))
+    s2 = fp4_scale_stepmajor(torch.randint(118, 124, (e, h, inter // 32), device=dev, dtype=torch.uint8))
+    per_expert = (2 * inter * h + h * inter) // 2 + s13[0].numel() + s2[0].numel()
+    recs += _moe_sweep(L, dev, "config4-shape mxfp4 moe", "ti_fp4_moe", w13, s13, w2, s2, e, h, inter, k,
+                       per_expert)
+    del w13, w2
+    torch.cuda.empty_cache()
+    return recs
+
+
+def _moe_sweep(L, dev, label, entry, w13, s13, w2, s2, e, h, inter, k, per_expert):
+    import torch
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    fn = getattr(L, entry)
+    recs = []
     for t in MOE_TS:
         g = torch.Generator(device=dev).manual_seed(t)
         x = torch.randn((t, h), generator=g, device=dev).to(torch.bfloat16)
@@ -325,9 +359,10 @@ def moe_points(dev, stream):
 
         def launch(st, t=t, x=x, logits=logits, wts=wts, ids=ids, out=out, wsp=wsp, need=need):
             _check("route", L.ti_moe_route_topk(logits.data_ptr(), t, e, k, 1, 1.0, wts.data_ptr(), ids.data_ptr(), st))
-            _check("moe", L.ti_fp8_moe(x.data_ptr(), wts.data_ptr(), ids.data_ptr(), t, k, w13.data_ptr(),
-                                       s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), e, h, inter, 0.0,
-                                       out.data_ptr(), wsp, need, st))
+            lay = (1,) if entry == "ti_fp4_moe" else ()
+            _check("moe", fn(x.data_ptr(), wts.data_ptr(), ids.data_ptr(), t, k, w13.data_ptr(),
+                             s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), *lay, e, h, inter, 0.0,
+                             out.data_ptr(), wsp, need, st))
 
         timed_burst([launch], 2, stream)
         reps = 10
@@ -336,11 +371,9 @@ def moe_points(dev, stream):
         touched = int(torch.unique(ids).numel())
         algo = touched * per_expert + t * h * 2 * 2
         flops = t * k * 2 * (2 * inter * h + h * inter)
-        recs.append(point_record(f"config4 fp8 moe T={t} experts_touched={touched}", ms * 1e-3, algo, flops, "hbm",
+        recs.append(point_record(f"{label} T={t} experts_touched={touched}", ms * 1e-3, algo, flops, "hbm",
                                  FP8_PEAK_TFLOPS))
         log(recs[-1])
-    del w13, w2
-    torch.cuda.empty_cache()
     return recs
 
 

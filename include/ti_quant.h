@@ -188,15 +188,23 @@ int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, const uint8_t* b,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* FP8 activations x MXFP4 weights: out[m,n] = sum_k a[m,k] * a_scale[m, k/128]
- * * w[n,k] * 2^(b_scale[n, k/32] - 127).  a e4m3 [M,K] with fp32 1x128 scales
+ * * w[n,k] * 2^(e[n, k/32] - 127).  a e4m3 [M,K] with fp32 1x128 scales
  * [M, K/128]; b e2m1 [N, K/2] (two values per byte along K, element 2i in the
- * low nibble -- torch float4_e2m1fn_x2); b_scale E8M0 bytes [N, K/32]; the
- * e8m0 scales are applied inside the MFMA (gfx950 block-scaled f8f6f4).
+ * low nibble -- torch float4_e2m1fn_x2); b_scale E8M0 bytes, layout 0 = the
+ * checkpoint's [N, K/32], layout 1 = step-major [K/128][N][4] (the 4 scales
+ * of a 128-wide K step of each row adjacent to the next row's, so a tile's
+ * scales are one contiguous read; build it once with ti_fp4_scale_stepmajor).
+ * The e8m0 scales are applied inside the MFMA (gfx950 block-scaled f8f6f4).
  * Replaces fp4_gemm (src/torchinferno/kernels/deepseek_v4_tilelang.py,
  * kernel deepseek_v4_tilelang_definitions.py:674-769).  K % 128 == 0. */
 int ti_fp4_gemm(const uint8_t* a, const float* a_scale, const uint8_t* b, const uint8_t* b_scale,
-                void* out, int out_dtype, int M, int N, int K, void* workspace, size_t workspace_bytes,
-                hipStream_t stream);
+                int b_scale_layout, void* out, int out_dtype, int M, int N, int K, void* workspace,
+                size_t workspace_bytes, hipStream_t stream);
+
+/* E8M0 scales [N, K/32] -> step-major [K/128][N][4] (weight preparation, run
+ * once per weight; no counterpart in the reference, whose kernels read the
+ * checkpoint layout). */
+int ti_fp4_scale_stepmajor(const uint8_t* src, int N, int K, uint8_t* dst, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Routed FP8 block-scaled MoE (DeepSeek expert shapes).
@@ -237,12 +245,13 @@ int ti_fp8_moe(const void* hidden, const float* topk_weights, const int32_t* top
  * (1x128 FP8 activations) -- the arithmetic of the reference's "tilelang-mxfp4"
  * expert path (Expert -> linear -> act_quant + fp4_gemm, tensor_parallel.py:
  * 195-207).  Replaces fused_mxfp4_moe (deepseek_v4_marlin.py:311-411).
- *   w13 e2m1 [E, 2I, H/2], s13 E8M0 [E, 2I, H/32]; w2 e2m1 [E, H, I/2],
- *   s2 E8M0 [E, H, I/32]; workspace as ti_fp8_moe_workspace_bytes. */
+ *   w13 e2m1 [E, 2I, H/2], s13 E8M0 per expert [2I, H/32] (scale_layout 0) or
+ *   step-major [H/128][2I][4] (scale_layout 1); w2 e2m1 [E, H, I/2], s2 per
+ *   expert [H, I/32] or [I/128][H][4]; workspace as ti_fp8_moe_workspace_bytes. */
 int ti_fp4_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids,
                int T, int k, const uint8_t* w13, const uint8_t* s13, const uint8_t* w2,
-               const uint8_t* s2, int E, int H, int I, float clamp_limit, void* out,
-               void* workspace, size_t workspace_bytes, hipStream_t stream);
+               const uint8_t* s2, int scale_layout, int E, int H, int I, float clamp_limit,
+               void* out, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

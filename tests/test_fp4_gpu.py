@@ -49,13 +49,26 @@ def test_fp4_gemm_matches_oracle(dev, m, n, k):
 @pytest.mark.parametrize("kind", ["1", "2", "3", "5", "6", "9"])
 @pytest.mark.parametrize("splits", ["1", "3"])
 def test_fp4_gemm_every_kind(dev, monkeypatch, kind, splits):
+    """Both scale layouts: the checkpoint's [N, K/32] and the step-major copy."""
     from torchinferno_amd.kernels import block_fp8 as tb
     print(f"[fp4] kind {kind} splits {splits}", flush=True)
     monkeypatch.setenv("TI_ROCM_FP8_KIND", kind)
     monkeypatch.setenv("TI_ROCM_FP8_SPLITS", splits)
     host, (a, a_s, b, b_s) = _inputs(77, 400, 1536, int(kind) * 10 + int(splits), dev)
+    ref = of4.fp4_gemm(*host)
     y = tb.fp4_gemm(a, a_s, b, b_s)
-    assert _rel_err(y.float().cpu().numpy(), of4.fp4_gemm(*host)) <= TOL
+    assert _rel_err(y.float().cpu().numpy(), ref) <= TOL
+    st = tb.fp4_scale_stepmajor(b_s.view(torch.uint8))
+    y2 = tb._fp4_gemm_raw(a, a_s, b, st, 1, 400)
+    assert torch.equal(y, y2)
+
+
+def test_fp4_scale_stepmajor_layout(dev):
+    from torchinferno_amd.kernels import block_fp8 as tb
+    s = torch.randint(0, 255, (3, 40, 64), dtype=torch.uint8)
+    st = tb.fp4_scale_stepmajor(s.to(dev)).cpu()
+    assert st.shape == (3, 16, 40, 4)
+    assert torch.equal(st, s.view(3, 40, 16, 4).permute(0, 2, 1, 3))
 
 
 def test_fp4_gemm_one_hot_exact(dev):
@@ -137,8 +150,10 @@ def test_mxfp4_moe_matches_oracle(dev, monkeypatch, t, k, kind):
     x = torch.randn((t, h), generator=g, device=dev).to(torch.bfloat16)
     w, ids = tmoe.route_topk(torch.randn((t, e), generator=g, device=dev), k)
     y = tmoe.fused_mxfp4_moe(x, w, ids, ex)
-    experts = [(ex.w13[i].cpu().numpy(), ex.w13_scale[i].cpu().numpy(), ex.w2[i].cpu().numpy(),
-                ex.w2_scale[i].cpu().numpy()) for i in range(e)]
+    def rows(st):  # step-major [K/128, N, 4] -> checkpoint [N, K/32]
+        return st.permute(1, 0, 2).reshape(st.size(1), -1).cpu().numpy()
+    experts = [(ex.w13[i].cpu().numpy(), rows(ex.w13_scale[i]), ex.w2[i].cpu().numpy(), rows(ex.w2_scale[i]))
+               for i in range(e)]
     ref = omoe.moe_reference(x.float().cpu().numpy(), w.cpu().numpy(), ids.cpu().numpy(), experts,
                              linear=omoe.mxfp4_linear)
     assert _rel_err(y.float().cpu().numpy(), ref) <= TOL

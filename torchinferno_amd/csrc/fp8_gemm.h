@@ -30,6 +30,7 @@ struct GemmArgs {
   const int* num_mtiles;    // device scalar: m-tiles in use
   long b_expert_stride;     // bytes between experts' [N, K] weights
   long sb_expert_stride;    // 4-byte units between experts' weight-scale grids
+  int sb_layout;            // SMODE 2: 0 = e8m0 [N, K/32]; 1 = step-major [K/128][N][4]
 };
 
 struct GemmPlan {

@@ -197,7 +197,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
   const uint8_t* dsrc[NI_HI];
   uint32_t dlds[NI_HI];
   bool dwide[NI_HI];
-  int dstep[NI_HI];  // source bytes per K step
+  int dstep[NI_HI];  // source bytes per K step; 0: a 4-byte scale per 128 K
 #pragma unroll
   for (int u = 0; u < NI_HI; ++u) {
     const int id = min(wave + u * W, NI - 1);
@@ -227,18 +227,23 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
       dsrc[u] = (const uint8_t*)(x.sa + row * KB);
       dlds[u] = (uint32_t)(A_BYTES + B_BYTES + j * 256);
       dwide[u] = false;
+      dstep[u] = 0;
     } else if constexpr (SMODE == 1) {
       const int nb = min(n0 / 128 + lane, (N + 127) / 128 - 1);
       dsrc[u] = (const uint8_t*)(sbmat + (long)nb * KB);
       dlds[u] = (uint32_t)(A_BYTES + B_BYTES + NI_SA * 256);
       dwide[u] = false;
+      dstep[u] = 0;
     } else {
-      // e8m0 bytes [N, K/32]: the row's dword of K step kk sits at byte 4*kk.
+      // e8m0 bytes, the row's dword of K step kk: [N, K/32] layout at byte
+      // nrow * K/32 + 4*kk (one dword per row: scattered), step-major
+      // [K/128][N][4] at byte (kk * N + nrow) * 4 (the tile's rows contiguous).
       const int j = id - NI_AB - NI_SA;
       const int nrow = min(n0 + j * 64 + lane, N - 1);
-      dsrc[u] = (const uint8_t*)sbmat + (long)nrow * (K / 32);
+      dsrc[u] = (const uint8_t*)sbmat + (x.sb_layout ? (long)nrow * 4 : (long)nrow * (K / 32));
       dlds[u] = (uint32_t)(A_BYTES + B_BYTES + SA_ROWS + j * 256);
       dwide[u] = false;
+      dstep[u] = x.sb_layout ? N * 4 : 4;
     }
   }
 
@@ -249,7 +254,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
     for (int u = 0; u < NI_HI; ++u) {
       if (wave + u * W >= NI) break;
       if (dwide[u]) dma16(dsrc[u] + kk * dstep[u], base + dlds[u]);
-      else dma4((const float*)dsrc[u] + kk * BK / 128, base + dlds[u]);
+      else dma4(dsrc[u] + (dstep[u] ? kk * dstep[u] : (kk * BK / 128) * 4), base + dlds[u]);
     }
   };
 
@@ -641,6 +646,7 @@ static int gemm_common(const char* name, int smode, const uint8_t* a, const floa
   GemmArgs x{};
   x.a = a; x.b = b; x.sa = a_scale; x.sb = b_scale;
   x.sa_stride = a_scale_stride; x.sb_stride = b_scale_stride;
+  x.sb_layout = smode == 2 ? b_scale_stride : 0;
   x.out = (uint16_t*)out;
   x.M = M; x.N = N; x.K = K;
   x.splits = p.splits; x.tiles_m = p.tiles_m; x.tiles_n = p.tiles_n; x.group_m = p.group_m;
@@ -694,8 +700,31 @@ extern "C" int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, const u
 }
 
 extern "C" int ti_fp4_gemm(const uint8_t* a, const float* a_scale, const uint8_t* b, const uint8_t* b_scale,
-                           void* out, int out_dtype, int M, int N, int K, void* workspace, size_t workspace_bytes,
-                           hipStream_t stream) {
-  return gemm_common("ti_fp4_gemm", 2, a, a_scale, 0, b, (const float*)b_scale, 0, out, out_dtype, M, N, K,
-                     workspace, workspace_bytes, stream);
+                           int b_scale_layout, void* out, int out_dtype, int M, int N, int K, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
+  TI_CHECK_ARG(b_scale_layout == 0 || b_scale_layout == 1, "ti_fp4_gemm: b_scale_layout must be 0 or 1");
+  return gemm_common("ti_fp4_gemm", 2, a, a_scale, 0, b, (const float*)b_scale, b_scale_layout, out, out_dtype, M,
+                     N, K, workspace, workspace_bytes, stream);
+}
+
+namespace {
+// [N, K/32] e8m0 -> step-major [K/128][N][4]: one thread per (step, row) dword.
+__global__ __launch_bounds__(256) void scale_stepmajor_kernel(const uint32_t* __restrict__ src, int N, int KS,
+                                                              uint32_t* __restrict__ dst) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)N * KS) return;
+  const int kk = (int)(i / N), n = (int)(i % N);
+  dst[i] = src[(long)n * KS + kk];
+}
+}  // namespace
+
+extern "C" int ti_fp4_scale_stepmajor(const uint8_t* src, int N, int K, uint8_t* dst, hipStream_t stream) {
+  TI_CHECK_ARG(src && dst, "ti_fp4_scale_stepmajor: null pointer");
+  TI_CHECK_SHAPE(N > 0 && K > 0 && K % 128 == 0, "ti_fp4_scale_stepmajor: need K %% 128 == 0 (N=%d K=%d)", N, K);
+  TI_CHECK_ARG(((uintptr_t)src & 3) == 0 && ((uintptr_t)dst & 3) == 0, "ti_fp4_scale_stepmajor: misaligned");
+  const long n = (long)N * (K / 128);
+  hipLaunchKernelGGL(scale_stepmajor_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     (const uint32_t*)src, N, K / 128, (uint32_t*)dst);
+  TI_CHECK_LAUNCH("ti_fp4_scale_stepmajor");
+  return TI_OK;
 }

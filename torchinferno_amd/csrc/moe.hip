@@ -327,7 +327,7 @@ extern "C" size_t ti_fp8_moe_workspace_bytes(int T, int k, int E, int H, int I) 
 // Routed experts, shared by the block-FP8 (smode 1: e4m3 weights, 128x128
 // fp32 scales) and MXFP4 (smode 2: e2m1 weights two per byte, e8m0 scale per
 // 32 K) weight formats; activations are 1x128 block FP8 in both.
-static int moe_run(const char* name, int smode, const void* hidden, const float* topk_weights,
+static int moe_run(const char* name, int smode, int sb_layout, const void* hidden, const float* topk_weights,
                    const int32_t* topk_ids, int T, int k, const uint8_t* w13, const void* s13, const uint8_t* w2,
                    const void* s2, int E, int H, int I, float clamp_limit, void* out, void* workspace,
                    size_t workspace_bytes, hipStream_t stream) {
@@ -361,6 +361,7 @@ static int moe_run(const char* name, int smode, const void* hidden, const float*
   // 3. grouped w13: [R, 2I] = xq[tok] . w13[e]^T
   fp8::GemmArgs g{};
   g.a = w.xq; g.sa = w.xs; g.b = w13; g.sb = (const float*)s13;
+  g.sb_layout = sb_layout;
   g.row_index = w.tok_of_pos;
   g.out = w.out1;
   g.M = (int)R; g.N = 2 * I; g.K = H;
@@ -399,14 +400,15 @@ extern "C" int ti_fp8_moe(const void* hidden, const float* topk_weights, const i
                           const uint8_t* w13, const float* s13, const uint8_t* w2, const float* s2, int E, int H,
                           int I, float clamp_limit, void* out, void* workspace, size_t workspace_bytes,
                           hipStream_t stream) {
-  return moe_run("ti_fp8_moe", 1, hidden, topk_weights, topk_ids, T, k, w13, s13, w2, s2, E, H, I, clamp_limit, out,
+  return moe_run("ti_fp8_moe", 1, 0, hidden, topk_weights, topk_ids, T, k, w13, s13, w2, s2, E, H, I, clamp_limit, out,
                  workspace, workspace_bytes, stream);
 }
 
 extern "C" int ti_fp4_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids, int T, int k,
-                          const uint8_t* w13, const uint8_t* s13, const uint8_t* w2, const uint8_t* s2, int E, int H,
-                          int I, float clamp_limit, void* out, void* workspace, size_t workspace_bytes,
-                          hipStream_t stream) {
-  return moe_run("ti_fp4_moe", 2, hidden, topk_weights, topk_ids, T, k, w13, s13, w2, s2, E, H, I, clamp_limit, out,
+                          const uint8_t* w13, const uint8_t* s13, const uint8_t* w2, const uint8_t* s2,
+                          int scale_layout, int E, int H, int I, float clamp_limit, void* out, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream) {
+  TI_CHECK_ARG(scale_layout == 0 || scale_layout == 1, "ti_fp4_moe: scale_layout must be 0 or 1");
+  return moe_run("ti_fp4_moe", 2, scale_layout, hidden, topk_weights, topk_ids, T, k, w13, s13, w2, s2, E, H, I, clamp_limit, out,
                  workspace, workspace_bytes, stream);
 }

@@ -109,6 +109,31 @@ def e8m0_bytes(scale: Tensor) -> Tensor:
     return b.contiguous().view(torch.uint8)
 
 
+def fp4_scale_stepmajor(scale_bytes: Tensor) -> Tensor:
+    """E8M0 bytes ``[..., N, K/32]`` -> step-major ``[..., K/128, N, 4]`` (one
+    contiguous read per tile and K step in the GEMM); weight preparation."""
+    _lib.require_device(scale_bytes)
+    *lead, n, kb = scale_bytes.shape
+    if kb % 4:
+        raise ValueError("MXFP4 scales need K divisible by 128")
+    src = scale_bytes.contiguous().view(-1, n, kb)
+    dst = torch.empty((src.size(0), kb // 4, n, 4), dtype=torch.uint8, device=src.device)
+    for i in range(src.size(0)):
+        _lib.call("ti_fp4_scale_stepmajor", src[i].data_ptr(), n, kb * 32, dst[i].data_ptr(),
+                  _lib.stream_of(src))
+    return dst.view(*lead, kb // 4, n, 4)
+
+
+def _fp4_gemm_raw(a: Tensor, a_s: Tensor, b: Tensor, eb: Tensor, layout: int, n: int) -> Tensor:
+    k = a.size(-1)
+    m = a.numel() // k
+    out = torch.empty((*a.shape[:-1], n), dtype=torch.bfloat16, device=a.device)
+    ws, ws_bytes = _ws_args(a.device, m, n, k, 2)
+    _lib.call("ti_fp4_gemm", a.data_ptr(), a_s.data_ptr(), b.data_ptr(), eb.data_ptr(), layout, out.data_ptr(),
+              _lib.TI_DTYPE_BF16, m, n, k, ws, ws_bytes, _lib.stream_of(a))
+    return out
+
+
 def fp4_gemm(
     a: Tensor,
     a_s: Tensor,
@@ -137,11 +162,7 @@ def fp4_gemm(
     eb = e8m0_bytes(b_s)
     if a_s.numel() != m * (k // BLOCK) or tuple(eb.shape) != (n, k // 32):
         raise ValueError("FP4 GEMM scales must be a_s [M, K/128] and b_s [N, K/32]")
-    out = torch.empty((*a.shape[:-1], n), dtype=torch.bfloat16, device=a.device)
-    ws, ws_bytes = _ws_args(a.device, m, n, k, 2)
-    _lib.call("ti_fp4_gemm", a.data_ptr(), a_s.data_ptr(), b.data_ptr(), eb.data_ptr(), out.data_ptr(),
-              _lib.TI_DTYPE_BF16, m, n, k, ws, ws_bytes, _lib.stream_of(a))
-    return out
+    return _fp4_gemm_raw(a, a_s, b, eb, 0, n)
 
 
 def linear(x: Tensor, weight: Tensor, weight_scale: Tensor) -> Tensor:
@@ -150,5 +171,16 @@ def linear(x: Tensor, weight: Tensor, weight_scale: Tensor) -> Tensor:
     ``fp4_gemm``, bf16 out."""
     xq, xs = act_quant(x)
     if weight.dtype == FP4:
-        return fp4_gemm(xq, xs, weight, weight_scale)
+        # The step-major copy of the weight's scales is built on first use and
+        # cached on the weight (like the reference's per-layer weight caches).
+        cached = getattr(weight, "_ti_fp4_scale_stepmajor", None)
+        if cached is None or cached[0] is not weight_scale:
+            eb = e8m0_bytes(weight_scale)
+            if eb.ndim != 2 or tuple(eb.shape) != (weight.size(0), weight.size(1) // 16):
+                raise ValueError("MXFP4 weight scale must be [N, K/32]")
+            cached = (weight_scale, fp4_scale_stepmajor(eb))
+            weight._ti_fp4_scale_stepmajor = cached
+        if xq.size(-1) != weight.size(1) * 2:
+            raise ValueError("MXFP4 weight K does not match the activation")
+        return _fp4_gemm_raw(xq.contiguous(), xs.contiguous(), weight, cached[1], 1, weight.size(0))
     return fp8_gemm(xq, xs, weight, weight_scale)

@@ -25,7 +25,7 @@ import torch
 from torch import Tensor
 
 from .. import _lib
-from .block_fp8 import FP4, e8m0_bytes
+from .block_fp8 import FP4, e8m0_bytes, fp4_scale_stepmajor
 from .fp8 import FP8_E4M3
 
 _ws_lock = threading.Lock()
@@ -83,9 +83,9 @@ class PreparedMxfp4Experts:
     """One GPU's MXFP4 experts in the kernel layout: ``w13 = [w1; w3]`` per expert."""
 
     w13: Tensor        # e2m1 x2 (uint8) [E, 2I, H/2]
-    w13_scale: Tensor  # E8M0 bytes [E, 2I, H/32]
+    w13_scale: Tensor  # E8M0 bytes, step-major [E, H/128, 2I, 4]
     w2: Tensor         # e2m1 x2 (uint8) [E, H, I/2]
-    w2_scale: Tensor   # E8M0 bytes [E, H, I/32]
+    w2_scale: Tensor   # E8M0 bytes, step-major [E, I/128, H, 4]
     expert_map: Tensor  # int32 [global experts] -> local index or -1
     global_num_experts: int
     hidden_size: int
@@ -98,7 +98,8 @@ def prepare_mxfp4_experts(w1: Tensor, w3: Tensor, w2: Tensor, w1_scale: Tensor, 
     """Stack one GPU's native MXFP4 experts (deepseek_v4_marlin.py:194-264, same
     arguments): ``w1``/``w3`` ``[E, I, H/2]`` and ``w2`` ``[E, H, I/2]``
     ``float4_e2m1fn_x2``; scales one E8M0 per 32 K (``[E, I, H/32]``,
-    ``[E, H, I/32]``).  No repacking: the kernels read the checkpoint layout."""
+    ``[E, H, I/32]``).  The weights keep the checkpoint layout; the scales are
+    rearranged once to the step-major layout the kernels read contiguously."""
     if w1.ndim != 3 or w3.ndim != 3 or w2.ndim != 3:
         raise ValueError("expert weights must be stacked [experts, output, packed-K]")
     if tuple(w1.shape) != tuple(w3.shape):
@@ -121,9 +122,9 @@ def prepare_mxfp4_experts(w1: Tensor, w3: Tensor, w2: Tensor, w1_scale: Tensor, 
     u8 = lambda t: t.contiguous().view(torch.uint8)  # noqa: E731
     return PreparedMxfp4Experts(
         w13=torch.cat((u8(w1), u8(w3)), dim=1).contiguous(),
-        w13_scale=torch.cat((s1, s3), dim=1).contiguous(),
+        w13_scale=fp4_scale_stepmajor(torch.cat((s1, s3), dim=1)),
         w2=u8(w2),
-        w2_scale=s2.contiguous(),
+        w2_scale=fp4_scale_stepmajor(s2),
         expert_map=expert_map,
         global_num_experts=global_num_experts,
         hidden_size=hidden,
@@ -180,9 +181,10 @@ def _routed(entry: str, hidden_states: Tensor, topk_weights: Tensor, topk_ids: T
     ws = _workspace(hidden_states.device, need)
     base = ws.data_ptr()
     aligned = (base + 255) & ~255
+    layout = (1,) if entry == "ti_fp4_moe" else ()  # MXFP4 scales are prepared step-major
     _lib.call(entry, hidden_states.data_ptr(), weights.data_ptr(), local_ids.data_ptr(), tokens, k,
               experts.w13.data_ptr(), experts.w13_scale.data_ptr(), experts.w2.data_ptr(),
-              experts.w2_scale.data_ptr(), e_local, hidden, inter, float(clamp_limit), out.data_ptr(),
+              experts.w2_scale.data_ptr(), *layout, e_local, hidden, inter, float(clamp_limit), out.data_ptr(),
               aligned, ws.numel() - (aligned - base), _lib.stream_of(hidden_states))
     return out
 
