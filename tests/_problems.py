@@ -17,3 +17,25 @@ def int4_problem(m: int, k: int, n: int, dtype: torch.dtype, seed: int):
 
 def to_np32(t: torch.Tensor) -> np.ndarray:
     return t.float().numpy()
+
+
+def pack_k_words(codes):
+    """GPTQ qweight: word [r, n] holds rows 8r..8r+7 of column n, row 8r+i in bits 4i."""
+    k, n = codes.shape
+    out = np.zeros((k // 8, n), np.uint32)
+    for r in range(k // 8):
+        for i in range(8):
+            out[r] |= codes[8 * r + i].astype(np.uint32) << np.uint32(4 * i)
+    return torch.from_numpy(out.view(np.int32))
+
+
+def pack_n_words(codes, order=None):
+    """Words along N: word [r, c] holds columns 8c..8c+7; slot j holds column
+    8c + order[j] (AWQ) or 8c + j (GPTQ qzeros)."""
+    r_, n = codes.shape
+    out = np.zeros((r_, n // 8), np.uint32)
+    for c in range(n // 8):
+        for j in range(8):
+            col = 8 * c + (order[j] if order else j)
+            out[:, c] |= codes[:, col].astype(np.uint32) << np.uint32(4 * j)
+    return torch.from_numpy(out.view(np.int32))

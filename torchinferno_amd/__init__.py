@@ -10,6 +10,7 @@ Python modules that mirror the reference's kernel API:
                            (src/torchinferno/kernels/deepseek_v4_tilelang.py)
 * ``kernels.moe``       -- softmax top-k router + routed FP8 MoE
                            (src/torchinferno/kernels/deepseek_v4_marlin.py)
+* ``kernels.checkpoint`` -- GPTQ / AWQ int4 ingestion, prepared-weight files
 * ``kernels.fused``     -- (add +) RMSNorm / SwiGLU -> per-token FP8 producers
                            (src/torchinferno/kernels/triton_ops.py:2127-2333)
 * ``ops``               -- torch.library custom ops over the above
