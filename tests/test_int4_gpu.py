@@ -164,6 +164,7 @@ _DECODE_PLANS = ["1:1:3:1", "2:1:4:3", "4:1:6:1", "1:2:3:2", "2:2:6:1", "4:2:4:2
 def test_decode_kernel_plans(dev, monkeypatch, plan, m):
     print(f"[int4] decode plan {plan} M={m}", flush=True)
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MIN_M", "1")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_WAVES", "4")
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_PLAN", plan)
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MR", "4" if m <= 4 else ("16" if m <= 16 else "32"))
     out, ref = _run_gemm(dev, m, 2048, 512, torch.float16 if m % 2 else torch.bfloat16, 20 + m)
@@ -199,15 +200,19 @@ def test_decode_four_row_override_ignored_above_four_rows(dev, monkeypatch, m):
     assert _rel_err(out.float().cpu().numpy(), ref) <= TOL
 
 
-# 8-wave tall tiles (64 rows, K halves on two waves per SIMD): each instantiated
-# (nt, ring), with and without split-K, ragged M, both dtypes, narrow and wide N.
-@pytest.mark.parametrize("plan", ["4:2:2:1", "4:2:2:3", "2:2:2:1", "2:2:3:1", "2:2:3:2"])
-@pytest.mark.parametrize("m,n", [(40, 512), (64, 1024), (100, 768), (128, 512)])
+# 8-wave tiles (two waves per SIMD, the K range split between them): every
+# instantiated (mr, nt, wk, ring), with and without split-K, ragged M, both
+# dtypes, narrow and wide N.
+@pytest.mark.parametrize("plan", ["64/4:2:2:1", "64/4:2:2:3", "64/2:2:2:1", "64/2:2:3:1", "64/2:2:3:2",
+                                  "32/4:4:2:1", "32/4:4:2:2", "32/2:2:3:1", "32/2:4:3:2", "32/1:4:3:1",
+                                  "32/1:4:3:3"])
+@pytest.mark.parametrize("m,n", [(40, 512), (64, 1024), (100, 768), (128, 512), (21, 256)])
 def test_decode_kernel_eight_waves(dev, monkeypatch, plan, m, n):
     print(f"[int4] 8-wave plan {plan} M={m} N={n}", flush=True)
+    mr, plan = plan.split("/")
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MIN_M", "1")
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MAX_M", "4096")
-    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MR", "64")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MR", mr)
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_WAVES", "8")
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_PLAN", plan)
     out, ref = _run_gemm(dev, m, 2048, n, torch.float16 if m % 2 else torch.bfloat16, 60 + m)

@@ -265,19 +265,12 @@ void launch_nt(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
   else launch_wk<DT, MR, 4>(p, x, stream);
 }
 
-// Tall tiles (64 / 128 staged rows) instantiate a curated set of
-// (nt, wk, ring) configurations -- 4 waves: (2,2,2), (4,1,2|3), (2,1,2|3|4);
-// 8 waves (two per SIMD, K split in halves, 64-row tiles only -- 128 rows do
-// not fit two stages): (4,2,2), (2,2,2|3); the plan only produces these.
+// Tall tiles (64 / 128 staged rows) on 4 waves instantiate a curated set of
+// (nt, wk, ring) configurations -- (2,2,2), (4,1,2|3), (2,1,2|3|4); the plan
+// only produces these.
 template <int DT, int MR>
 void launch_tall(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
-  if (MR == 64 && p.waves == 8) {
-    if constexpr (MR == 64) {
-      if (p.nt == 4) launch_split<DT, MR, 4, 2, 2, 8>(p, x, stream);
-      else if (p.ring == 2) launch_split<DT, MR, 2, 2, 2, 8>(p, x, stream);
-      else launch_split<DT, MR, 2, 2, 3, 8>(p, x, stream);
-    }
-  } else if (p.wk == 2) launch_split<DT, MR, 2, 2, 2>(p, x, stream);
+  if (p.wk == 2) launch_split<DT, MR, 2, 2, 2>(p, x, stream);
   else if (p.nt == 4) {
     if (p.ring == 2) launch_split<DT, MR, 4, 1, 2>(p, x, stream);
     else launch_split<DT, MR, 4, 1, 3>(p, x, stream);
@@ -288,8 +281,27 @@ void launch_tall(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
   }
 }
 
+// 8-wave workgroups (two waves per SIMD), the configurations of kEight.
+template <int DT>
+void launch_eight(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
+  if (p.mr == 64) {
+    if (p.nt == 4) launch_split<DT, 64, 4, 2, 2, 8>(p, x, stream);
+    else if (p.ring == 2) launch_split<DT, 64, 2, 2, 2, 8>(p, x, stream);
+    else launch_split<DT, 64, 2, 2, 3, 8>(p, x, stream);
+  } else {
+    if (p.nt == 4) launch_split<DT, 32, 4, 4, 2, 8>(p, x, stream);
+    else if (p.nt == 1) launch_split<DT, 32, 1, 4, 3, 8>(p, x, stream);
+    else if (p.wk == 2) launch_split<DT, 32, 2, 2, 3, 8>(p, x, stream);
+    else launch_split<DT, 32, 2, 4, 3, 8>(p, x, stream);
+  }
+}
+
 template <int DT>
 void launch_mr(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
+  if (p.waves == 8) {
+    launch_eight<DT>(p, x, stream);
+    return;
+  }
   if (p.mr == 4) launch_nt<DT, 4>(p, x, stream);
   else if (p.mr == 16) launch_nt<DT, 16>(p, x, stream);
   else if (p.mr == 32) launch_nt<DT, 32>(p, x, stream);
@@ -298,6 +310,20 @@ void launch_mr(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
 }
 
 int stage_bytes(int mr, int nt, int wk, int waves) { return waves * nt * 1024 + wk * mr * 256; }
+
+// The instantiated 8-wave configurations (mr, nt, wk, ring): 64-row tiles with
+// the K range halved, 32-row tiles with it halved or quartered.
+struct EightCfg {
+  int mr, nt, wk, ring;
+};
+constexpr EightCfg kEight[] = {{64, 4, 2, 2}, {64, 2, 2, 2}, {64, 2, 2, 3}, {32, 4, 4, 2},
+                               {32, 2, 2, 3}, {32, 2, 4, 3}, {32, 1, 4, 3}};
+
+bool eight_instantiated(const DecodePlan& p) {
+  for (const EightCfg& c : kEight)
+    if (c.mr == p.mr && c.nt == p.nt && c.wk == p.wk && c.ring == p.ring) return true;
+  return false;
+}
 
 // TI_ROCM_W4A16_DECODE_PLAN="nt:wk:ring:splits" overrides the heuristic (tuning).
 bool env_plan(DecodePlan& p) {
@@ -312,15 +338,26 @@ bool env_plan(DecodePlan& p) {
 // Completes a plan: snaps (nt, wk, ring) to an instantiated configuration,
 // tiles N, caps splits and sizes the LDS (ring, staged scales, WK reduction).
 DecodePlan finish_decode_plan(DecodePlan p, int N, int NG, bool tall) {
-  if (tall && p.waves == 8) {
-    // 8 waves = 2 K halves x 4 column sets: (4,2,2) covers 256 columns,
-    // (2,2,2|3) 128.
-    p.wk = 2;
-    if (p.nt >= 4 && N % 256 == 0) { p.nt = 4; p.ring = 2; }
-    else { p.nt = 2; p.ring = p.ring >= 3 ? 3 : 2; }
-    if (N % (4 * p.nt * 16)) { p.waves = kWaves; p.wk = 1; }  // the 4-wave table below
+  if (p.waves == 8) {
+    // Snap to a kEight entry of this mr: the requested (nt, wk) if listed
+    // (its ring), else the first whose columns tile N; none -> 4 waves.
+    const EightCfg* pick = nullptr;
+    for (const EightCfg& c : kEight)
+      if (c.mr == p.mr && c.nt == p.nt && c.wk == p.wk && N % (8 / c.wk * c.nt * 16) == 0 &&
+          (!pick || c.ring == p.ring))
+        pick = &c;
+    for (const EightCfg& c : kEight)
+      if (!pick && c.mr == p.mr && N % (8 / c.wk * c.nt * 16) == 0) pick = &c;
+    if (pick) {
+      p.nt = pick->nt; p.wk = pick->wk; p.ring = pick->ring;
+    } else {
+      p.waves = kWaves;
+      p.wk = 1;
+    }
   }
-  if (tall && p.waves != 8) {
+  if (p.waves == 8) {
+    // fixed by the table entry
+  } else if (tall) {
     // The instantiated tall configurations: (2,2,2), (4,1,2|3), (2,1,2|3|4); a
     // workgroup covers 256 / 128 / 64 columns, which must divide N.
     if (p.wk == 1 && p.nt >= 4 && N % 256) p.nt = 2;
@@ -341,7 +378,9 @@ DecodePlan finish_decode_plan(DecodePlan p, int N, int NG, bool tall) {
   const int wc = p.waves / p.wk * p.nt * 16;
   const int sbytes = cdiv(ngr * wc * 2, 256) * 256;
   auto fits = [&](int r) { return r * stage_bytes(p.mr, p.nt, p.wk, p.waves) + sbytes <= kDecodeLdsMax; };
-  if (tall) {
+  if (p.waves == 8) {
+    // the table's ring; an oversized plan is stepped down by the caller
+  } else if (tall) {
     while (p.ring > 2 && !fits(p.ring)) p.ring = p.ring == 4 ? 3 : 2;
   } else {
     while (p.ring > 3 && !fits(p.ring)) p.ring = p.ring == 6 ? 4 : 3;
@@ -370,10 +409,11 @@ DecodePlan make_decode_plan(int M, int N, int K) {
   }
   const bool tall = p.mr >= 64;
   p.mchunks = cdiv(M, p.mr > 16 ? p.mr : 16);
-  // Wide N above 32 rows: 64-row tiles on 8 waves (two per SIMD, the K range
-  // halved between them) -- measured 17% (M=64) / 7% (M=128) faster than the
-  // best 4-wave plans at the Llama-3-8B gate_up shape.
-  p.waves = (p.mr == 64 && wide) ? 8 : kWaves;
+  // 32- and 64-row tiles run on 8 waves (two per SIMD, the K range split
+  // between them): one wave per SIMD serializes its VALU unpack, MFMAs and LDS
+  // waits.  Measured 7-19% faster than the best 4-wave plans at the
+  // Llama-3-8B MLP shapes (M = 32..128).
+  p.waves = ((p.mr == 64 && wide) || p.mr == 32) ? 8 : kWaves;
   const int NG = K / kGroup;
   if (!env_plan(p)) {
     // Measured on MI355X at the Llama-3-8B MLP shapes, rows 17..128: wide N
@@ -382,12 +422,19 @@ DecodePlan make_decode_plan(int M, int N, int K) {
     p.splits = 1;
     p.ring = 3;
     if (tall) {
-      p.nt = (p.waves == 8 && M <= 64) ? 2 : 4; p.wk = 1; p.ring = 2;
+      p.nt = (p.waves == 8 && M <= 64) ? 2 : 4; p.wk = p.waves == 8 ? 2 : 1; p.ring = 2;
       const int blocks = max(1, cdiv(T, kWaves * p.nt)) * p.mchunks;
       p.splits = blocks >= 192 ? 1 : cdiv(256, blocks);
     } else if (wide) {
-      if (M <= 32) { p.nt = 4; p.wk = 2; }
+      if (p.waves == 8) { p.nt = 2; p.wk = 2; p.ring = 3; }
+      else if (M <= 32) { p.nt = 4; p.wk = 2; }
       else { p.nt = 2; p.wk = 1; p.ring = 4; }
+    } else if (p.waves == 8) {
+      // narrow N: K in quarters, 2-way split-K; wider column sets as M grows
+      p.wk = 4; p.splits = 2;
+      if (M <= 32) { p.nt = 1; p.ring = 3; }
+      else if (M <= 64) { p.nt = 2; p.ring = 3; }
+      else { p.nt = 4; p.ring = 2; }
     } else {
       p.wk = 4;
       p.nt = M <= 64 ? 2 : 4;
@@ -396,12 +443,13 @@ DecodePlan make_decode_plan(int M, int N, int K) {
     }
   }
   const char* ew = getenv("TI_ROCM_W4A16_DECODE_WAVES");
-  if (ew && *ew && p.mr == 64) p.waves = atoi(ew) == 8 ? 8 : kWaves;
+  if (ew && *ew && (p.mr == 32 || p.mr == 64)) p.waves = atoi(ew) == 8 ? 8 : kWaves;
   DecodePlan q = finish_decode_plan(p, N, NG, tall);
   // An 8-wave plan whose LDS (ring + the staged scale slab, which grows with
-  // K) does not fit steps down to 128 columns, then to the 4-wave table.
-  if (q.waves == 8 && q.lds > kDecodeLdsMax && q.nt == 4) {
-    p.nt = 2;
+  // K) does not fit steps down to half the columns, then to the 4-wave table.
+  if (q.waves == 8 && q.lds > kDecodeLdsMax && q.nt >= 2) {
+    p.nt = q.nt / 2;
+    p.wk = q.wk;
     q = finish_decode_plan(p, N, NG, tall);
   }
   if (q.waves == 8 && q.lds > kDecodeLdsMax) {
@@ -416,8 +464,7 @@ bool decode_plan_valid(const DecodePlan& p, int N) {
   if (p.waves != 4 && p.waves != 8) return false;
   if (N % (p.waves / p.wk * p.nt * 16) || p.nblocks * (p.waves / p.wk * p.nt * 16) != N) return false;
   if (p.lds > kDecodeLdsMax) return false;
-  if (p.waves == 8)
-    return p.mr == 64 && p.wk == 2 && ((p.nt == 4 && p.ring == 2) || (p.nt == 2 && (p.ring == 2 || p.ring == 3)));
+  if (p.waves == 8) return eight_instantiated(p);
   if (p.mr >= 64)
     return (p.nt == 2 && p.wk == 2 && p.ring == 2) || (p.nt == 4 && p.wk == 1 && (p.ring == 2 || p.ring == 3)) ||
            (p.nt == 2 && p.wk == 1 && (p.ring >= 2 && p.ring <= 4));
