@@ -57,7 +57,7 @@ __global__ __launch_bounds__(64 * KW) void w4a16_decode_kernel(
   __shared__ int last_flag;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar
   const int wk = wave / WN, wn = wave % WN;
   const int nb = blockIdx.x, split = blockIdx.y, mchunk = blockIdx.z;
   const int NG = K / kGroup;
@@ -97,24 +97,35 @@ __global__ __launch_bounds__(64 * KW) void w4a16_decode_kernel(
     }
   }
 
-  // Issue the DMAs of step `i` into ring buffer i % R.
+  // Issue the DMAs of step `i` into ring buffer i % R.  Per-lane byte offsets
+  // are fixed for the whole walk (computed here, once); per step only the
+  // wave-uniform group base moves, in scalar registers.
+  uint32_t woff[NT], aoff[AI_HI];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) woff[t] = (uint32_t)(((tile0 + t) * 64 + lane) * 16);
+#pragma unroll
+  for (int u = 0; u < AI_HI; ++u) {
+    const int id = min(wave + u * KW, AI - 1);
+    const int k4 = id % (MR / 4);
+    const int r = 4 * k4 + (lane >> 4);
+    const int q = (lane & 15) ^ (r & 15);
+    const int row = min(m0 + r, M - 1);
+    aoff[u] = (uint32_t)(((long)row * K + q * 8) * 2);
+  }
   auto issue = [&](int i) {
     const uint32_t base = ring0 + (uint32_t)((i % R) * STAGE);
     const int g = min(g0 + wk * nper + i, gmax);
+    const char* wbase = (const char*)Wp + (long)g * T * 1024;
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-      dma16(&Wp[((long)g * T + tile0 + t) * 64 + lane], base + (uint32_t)((wave * NT + t) * 1024));
+    for (int t = 0; t < NT; ++t) dma16_sv(wbase, woff[t], base + (uint32_t)((wave * NT + t) * 1024));
 #pragma unroll
     for (int u = 0; u < AI_HI; ++u) {
       const int id = wave + u * KW;        // 0 .. AI - 1
       if (id >= AI) break;
       const int awk = id / (MR / 4), k4 = id % (MR / 4);
-      const int r = 4 * k4 + (lane >> 4);
-      const int q = (lane & 15) ^ (r & 15);
       const int ga = min(g0 + awk * nper + i, gmax);
-      const int row = min(m0 + r, M - 1);
-      dma16(A + (long)row * K + (long)ga * kGroup + q * 8,
-            base + (uint32_t)(W_BYTES + awk * A_BYTES + k4 * 1024));
+      dma16_sv((const char*)A + (long)ga * kGroup * 2, aoff[u],
+               base + (uint32_t)(W_BYTES + awk * A_BYTES + k4 * 1024));
     }
   };
 

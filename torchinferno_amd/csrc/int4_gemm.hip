@@ -539,8 +539,10 @@ static int env_int(const char* name, int dflt) {
   return (e && *e) ? atoi(e) : dflt;
 }
 
-static bool use_decode(int M) {
-  return M >= env_int("TI_ROCM_W4A16_DECODE_MIN_M", 17) && M <= env_int("TI_ROCM_W4A16_DECODE_MAX_M", 128);
+// The decode kernel addresses activations with 32-bit byte offsets (M*K*2 < 2^31).
+static bool use_decode(int M, int K) {
+  return M >= env_int("TI_ROCM_W4A16_DECODE_MIN_M", 17) && M <= env_int("TI_ROCM_W4A16_DECODE_MAX_M", 128) &&
+         (long)M * K * 2 < (1L << 31);
 }
 
 // Workspace of one call: fp32 partials [splits][M][N] from the start, ticket
@@ -553,7 +555,7 @@ struct WsNeed {
 };
 
 static WsNeed ws_need(int M, int N, int K) {
-  if (use_decode(M)) {
+  if (use_decode(M, K)) {
     DecodePlan d = make_decode_plan(M, N, K);
     if (d.splits <= 1) return {0, 0};
     return {decode_partial_bytes(d, M, N), decode_ticket_bytes(d)};
@@ -567,7 +569,7 @@ extern "C" int ti_w4a16_plan_name(int M, int N, int K, int group_size, char* buf
   TI_CHECK_ARG(buf && len > 0, "ti_w4a16_plan_name: null buffer");
   TI_CHECK_SHAPE(group_size == kGroup && M >= 1 && N > 0 && K > 0 && K % kGroup == 0 && N % 64 == 0,
                  "ti_w4a16_plan_name: need M >= 1, K %% 128 == 0, N %% 64 == 0");
-  if (use_decode(M)) {
+  if (use_decode(M, K)) {
     DecodePlan d = make_decode_plan(M, N, K);
     snprintf(buf, len, "w4a16_decode_kernel mr=%d nt=%d wk=%d waves=%d ring=%d splits=%d mchunks=%d lds=%d", d.mr,
              d.nt, d.wk, d.waves, d.ring, d.splits, d.mchunks, d.lds);
@@ -678,7 +680,7 @@ extern "C" int ti_w4a16_gemm(const void* a, int dtype, const int32_t* packed_wei
                ((uintptr_t)packed_scales & 15) == 0,
                "ti_w4a16_gemm: a, packed_weight and packed_scales must be 16-byte aligned");
   TI_CHECK_ARG(((uintptr_t)out & 7) == 0, "ti_w4a16_gemm: out must be 8-byte aligned");
-  if (use_decode(M)) {
+  if (use_decode(M, K)) {
     DecodePlan d = make_decode_plan(M, N, K);
     TI_CHECK_SHAPE(d.lds <= kDecodeLdsMax, "ti_w4a16_gemm: decode plan needs %d bytes of LDS", d.lds);
     TI_CHECK_SHAPE(decode_plan_valid(d, N), "ti_w4a16_gemm: no decode kernel for plan nt=%d wk=%d ring=%d mr=%d at N=%d",

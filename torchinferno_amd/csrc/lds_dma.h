@@ -24,6 +24,16 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
                : "memory");
 }
 
+// 16 bytes per lane from a wave-uniform base plus a 32-bit per-lane byte offset
+// (the scalar-base form: the base lives in SGPRs, so a loop that only moves the
+// base spends no vector instructions on addresses).
+__device__ __forceinline__ void dma16_sv(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds_base))
+               : "memory");
+}
+
 // 4 bytes per lane: global g -> LDS at lds_base + 4 * lane.
 __device__ __forceinline__ void dma4(const void* g, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
