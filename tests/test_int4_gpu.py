@@ -205,7 +205,8 @@ def test_decode_four_row_override_ignored_above_four_rows(dev, monkeypatch, m):
 # dtypes, narrow and wide N.
 @pytest.mark.parametrize("plan", ["64/4:2:2:1", "64/4:2:2:3", "64/2:2:2:1", "64/2:2:3:1", "64/2:2:3:2",
                                   "32/4:4:2:1", "32/4:4:2:2", "32/2:2:3:1", "32/2:4:3:2", "32/1:4:3:1",
-                                  "32/1:4:3:3"])
+                                  "32/1:4:3:3", "16/4:2:3:1", "16/4:2:3:2", "16/2:2:4:1", "16/2:4:4:3",
+                                  "16/1:4:6:2"])
 @pytest.mark.parametrize("m,n", [(40, 512), (64, 1024), (100, 768), (128, 512), (21, 256)])
 def test_decode_kernel_eight_waves(dev, monkeypatch, plan, m, n):
     print(f"[int4] 8-wave plan {plan} M={m} N={n}", flush=True)

@@ -299,6 +299,11 @@ void launch_eight(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) 
     if (p.nt == 4) launch_split<DT, 64, 4, 2, 2, 8>(p, x, stream);
     else if (p.ring == 2) launch_split<DT, 64, 2, 2, 2, 8>(p, x, stream);
     else launch_split<DT, 64, 2, 2, 3, 8>(p, x, stream);
+  } else if (p.mr == 16) {
+    if (p.nt == 4) launch_split<DT, 16, 4, 2, 3, 8>(p, x, stream);
+    else if (p.nt == 1) launch_split<DT, 16, 1, 4, 6, 8>(p, x, stream);
+    else if (p.wk == 2) launch_split<DT, 16, 2, 2, 4, 8>(p, x, stream);
+    else launch_split<DT, 16, 2, 4, 4, 8>(p, x, stream);
   } else {
     if (p.nt == 4) launch_split<DT, 32, 4, 4, 2, 8>(p, x, stream);
     else if (p.nt == 1) launch_split<DT, 32, 1, 4, 3, 8>(p, x, stream);
@@ -328,7 +333,8 @@ struct EightCfg {
   int mr, nt, wk, ring;
 };
 constexpr EightCfg kEight[] = {{64, 4, 2, 2}, {64, 2, 2, 2}, {64, 2, 2, 3}, {32, 4, 4, 2},
-                               {32, 2, 2, 3}, {32, 2, 4, 3}, {32, 1, 4, 3}};
+                               {32, 2, 2, 3}, {32, 2, 4, 3}, {32, 1, 4, 3}, {16, 4, 2, 3},
+                               {16, 2, 2, 4}, {16, 2, 4, 4}, {16, 1, 4, 6}};
 
 bool eight_instantiated(const DecodePlan& p) {
   for (const EightCfg& c : kEight)
@@ -424,10 +430,10 @@ DecodePlan make_decode_plan(int M, int N, int K) {
   // between them): one wave per SIMD serializes its VALU unpack, MFMAs and LDS
   // waits.  Measured 7-19% faster than the best 4-wave plans at the
   // Llama-3-8B MLP shapes (M = 32..128).
-  p.waves = ((p.mr == 64 && wide) || p.mr == 32) ? 8 : kWaves;
+  p.waves = ((p.mr == 64 && wide) || p.mr == 32 || p.mr == 16) ? 8 : kWaves;
   const int NG = K / kGroup;
   if (!env_plan(p)) {
-    // Measured on MI355X at the Llama-3-8B MLP shapes, rows 17..128: wide N
+    // Measured on MI355X at the Llama-3-8B MLP shapes, rows 9..128: wide N
     // (gate_up, N=28672) streams with whole-K workgroups; narrow N (down,
     // N=4096) puts all four waves on K (and a 2-way split at M <= 32).
     p.splits = 1;
@@ -437,13 +443,14 @@ DecodePlan make_decode_plan(int M, int N, int K) {
       const int blocks = max(1, cdiv(T, kWaves * p.nt)) * p.mchunks;
       p.splits = blocks >= 192 ? 1 : cdiv(256, blocks);
     } else if (wide) {
-      if (p.waves == 8) { p.nt = 2; p.wk = 2; p.ring = 3; }
+      if (p.waves == 8) { p.nt = 2; p.wk = 2; p.ring = p.mr == 16 ? 4 : 3; }
       else if (M <= 32) { p.nt = 4; p.wk = 2; }
       else { p.nt = 2; p.wk = 1; p.ring = 4; }
     } else if (p.waves == 8) {
       // narrow N: K in quarters, 2-way split-K; wider column sets as M grows
       p.wk = 4; p.splits = 2;
-      if (M <= 32) { p.nt = 1; p.ring = 3; }
+      if (M <= 16) { p.nt = 1; p.ring = 6; }
+      else if (M <= 32) { p.nt = 1; p.ring = 3; }
       else if (M <= 64) { p.nt = 2; p.ring = 3; }
       else { p.nt = 4; p.ring = 2; }
     } else {
@@ -454,7 +461,7 @@ DecodePlan make_decode_plan(int M, int N, int K) {
     }
   }
   const char* ew = getenv("TI_ROCM_W4A16_DECODE_WAVES");
-  if (ew && *ew && (p.mr == 32 || p.mr == 64)) p.waves = atoi(ew) == 8 ? 8 : kWaves;
+  if (ew && *ew && (p.mr == 16 || p.mr == 32 || p.mr == 64)) p.waves = atoi(ew) == 8 ? 8 : kWaves;
   DecodePlan q = finish_decode_plan(p, N, NG, tall);
   // An 8-wave plan whose LDS (ring + the staged scale slab, which grows with
   // K) does not fit steps down to half the columns, then to the 4-wave table.

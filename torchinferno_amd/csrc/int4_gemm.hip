@@ -180,7 +180,7 @@ __global__ __launch_bounds__(64 * W) void w4a16_gemm_kernel(
   __shared__ int last_flag;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar
   const int nb = blockIdx.x;
   const int split = blockIdx.y;
   const int mchunk = blockIdx.z;
@@ -531,8 +531,8 @@ extern "C" int ti_int4_dequant(const int32_t* packed_weight, const void* packed_
 }
 
 // Kernel choice by M (measured on MI355X at the Llama-3-8B MLP shapes): the
-// register-ring kernel of this file streams best for M <= 16; the LDS-DMA
-// decode kernel (int4_decode.hip) for 17 <= M <= 128; above, this file's kernel
+// register-ring kernel of this file streams best for M <= 8; the LDS-DMA
+// decode kernel (int4_decode.hip) for 9 <= M <= 128; above, this file's kernel
 // again.  TI_ROCM_W4A16_DECODE_MIN_M / _MAX_M override the range (tuning).
 static int env_int(const char* name, int dflt) {
   const char* e = getenv(name);
@@ -541,7 +541,7 @@ static int env_int(const char* name, int dflt) {
 
 // The decode kernel addresses activations with 32-bit byte offsets (M*K*2 < 2^31).
 static bool use_decode(int M, int K) {
-  return M >= env_int("TI_ROCM_W4A16_DECODE_MIN_M", 17) && M <= env_int("TI_ROCM_W4A16_DECODE_MAX_M", 128) &&
+  return M >= env_int("TI_ROCM_W4A16_DECODE_MIN_M", 9) && M <= env_int("TI_ROCM_W4A16_DECODE_MAX_M", 128) &&
          (long)M * K * 2 < (1L << 31);
 }
 
