@@ -447,8 +447,10 @@ DecodePlan make_decode_plan(int M, int N, int K) {
       else if (M <= 32) { p.nt = 4; p.wk = 2; }
       else { p.nt = 2; p.wk = 1; p.ring = 4; }
     } else if (p.waves == 8) {
-      // narrow N: K in quarters, 2-way split-K; wider column sets as M grows
-      p.wk = 4; p.splits = 2;
+      // narrow N: K in quarters, 2-way split-K when K is deep (>= 64 groups:
+      // the down projection; a 4096-deep K measured faster unsplit); wider
+      // column sets as M grows
+      p.wk = 4; p.splits = NG >= 64 ? 2 : 1;
       if (M <= 16) { p.nt = 1; p.ring = 6; }
       else if (M <= 32) { p.nt = 1; p.ring = 3; }
       else if (M <= 64) { p.nt = 2; p.ring = 3; }
