@@ -1,0 +1,62 @@
+"""The C ABI allocates nothing and clears nothing with memsets (split-K tickets
+are left at zero by the kernels themselves), so calls can be captured into a HIP
+graph.  Captured int4 (split-K), FP8 (split-K), fused-producer and MoE calls are
+replayed several times, with eager work and synchronizations between the
+replays, and every replay must equal the eager result bit for bit."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def test_graph_replays_match_eager(dev, monkeypatch):
+    from torchinferno_amd.kernels import fp8 as tf8
+    from torchinferno_amd.kernels import fused
+    from torchinferno_amd.kernels import int4 as ti4
+    from torchinferno_amd.kernels import moe as tmoe
+    from tests.test_moe_gpu import _make_experts
+
+    g = torch.Generator(device=dev).manual_seed(3)
+    # int4, a split-K plan (narrow N, deep K)
+    k4, n4, m4 = 14336, 512, 4
+    q, s = ti4.quantize_to_int4((torch.randn((k4, n4), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+    ws4 = ti4.make_workspace(n4, dev, size_k=k4, max_m=m4)
+    a4 = torch.randn((m4, k4), generator=g, device=dev).to(torch.bfloat16)
+    assert ti4.workspace_bytes(m4, n4, k4) > 0, "the case must exercise split-K"
+    # FP8 row/col, a split-K plan (M=1)
+    wq, wsc = tf8.quantize_weight_fp8_per_channel(
+        (torch.randn((1024, 8192), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+    x8 = torch.randn((1, 8192), generator=g, device=dev).to(torch.bfloat16)
+    # fused producer, MoE
+    gu = torch.randn((6, 2 * 2048), generator=g, device=dev).to(torch.bfloat16)
+    ex = _make_experts(8, 256, 256, 5, dev)
+    xm = torch.randn((12, 256), generator=g, device=dev).to(torch.bfloat16)
+    logits = torch.randn((12, 8), generator=g, device=dev)
+
+    def run():
+        y4 = ti4.int4_mm(a4, q, s, ws4, n4, k4)
+        xq, xs = tf8.quantize_activation_fp8_per_token(x8)
+        y8 = tf8.fp8_per_token_linear_quantized(xq, xs, wq, wsc, out_dtype=torch.bfloat16)
+        fq, fs = fused.swiglu_fp8_per_token(*gu.split(2048, dim=-1))
+        ym = tmoe.moe_forward(xm, logits, ex, 2)
+        return y4, y8, fq.view(torch.uint8), fs, ym
+
+    eager = [t.clone() for t in run()]
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        run()  # warm-up on the capture stream (workspaces already sized)
+    torch.cuda.current_stream(dev).wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        outs = run()
+    for rep in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, ref in zip(outs, eager):
+            assert torch.equal(got, ref), f"replay {rep} differs"
+        # eager work between replays, using the same workspaces
+        assert torch.equal(ti4.int4_mm(a4, q, s, ws4, n4, k4), eager[0])
+        torch.cuda.synchronize()
