@@ -229,7 +229,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
       dwide[u] = false;
       dstep[u] = 0;
     } else if constexpr (SMODE == 1) {
-      const int nb = min(n0 / 128 + lane, (N + 127) / 128 - 1);
+      // Only the tile's BN/128 column blocks are read; the other lanes repeat
+      // the last one (one cache line per step instead of 64).
+      const int nb = min(n0 / 128 + min(lane, (BN + 127) / 128 - 1), (N + 127) / 128 - 1);
       dsrc[u] = (const uint8_t*)(sbmat + (long)nb * KB);
       dlds[u] = (uint32_t)(A_BYTES + B_BYTES + NI_SA * 256);
       dwide[u] = false;
