@@ -229,7 +229,8 @@ def fp8_points(dev, stream):
                       for _ in range(ncopy)]
             for m in ms:
                 a = torch.randint(-120, 120, (m, k), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
-                asc = torch.rand((m,) if mode == 0 else (m, k // 128), device=dev) * 0.01 + 1e-3
+                # modes 1/2: step-major activation scales [K/128, M], as the DSv4 linear path keeps them
+                asc = torch.rand((m,) if mode == 0 else (k // 128, m), device=dev) * 0.01 + 1e-3
                 out = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
                 i = [0]
 
@@ -240,10 +241,10 @@ def fp8_points(dev, stream):
                         r = L.ti_fp8_gemm_rowcol(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(),
                                                  1, out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
                     elif mode == 2:
-                        r = L.ti_fp4_gemm(a.data_ptr(), asc.data_ptr(), bq[j].data_ptr(), bs[j].data_ptr(), 1,
+                        r = L.ti_fp4_gemm(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(), 1,
                                           out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
                     else:
-                        r = L.ti_fp8_gemm_block(a.data_ptr(), asc.data_ptr(), bq[j].data_ptr(), bs[j].data_ptr(),
+                        r = L.ti_fp8_gemm_block(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(),
                                                 out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
                     _check("fp8 gemm", r)
 

@@ -120,9 +120,11 @@ int ti_fp8_quant_per_token(const void* x, int x_dtype, int M, int K, float eps,
  * s = max(amax, 1e-4) * (1/448) -- or 2^ceil(log2(that)) if round_scale --
  * xq = e4m3(clamp(x / s, -448, 448)).  Replaces act_quant
  * (src/torchinferno/kernels/deepseek_v4_tilelang.py:147-173, kernel
- * deepseek_v4_tilelang_definitions.py:273-331).  xs [M, K/128]. */
+ * deepseek_v4_tilelang_definitions.py:273-331).  xs [M, K/128] for
+ * scale_layout 0 (the reference's), [K/128, M] ("step-major") for 1, the
+ * layout the block and FP4 GEMMs read fastest. */
 int ti_fp8_quant_block(const void* x, int x_dtype, int M, int K, int block_size,
-                       int round_scale, uint8_t* xq, float* xs, hipStream_t stream);
+                       int round_scale, uint8_t* xq, float* xs, int scale_layout, hipStream_t stream);
 
 /* Tensor-scale cast xq = e4m3(x * inv_scale[0]) over n elements (n % 8 == 0).
  * Replaces the Triton _scale_cast_fp8 of quantize_activation_fp8
@@ -183,7 +185,7 @@ int ti_fp8_gemm_rowcol(const uint8_t* a, const float* a_scale, int a_scale_per_r
  * b_scale[n/128, kb]; a_scale [M, K/128], b_scale [ceil(N/128), K/128], fp32.
  * Replaces fp8_gemm (src/torchinferno/kernels/deepseek_v4_tilelang.py:207-223,
  * kernel deepseek_v4_tilelang_definitions.py:436-485). */
-int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, const uint8_t* b,
+int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, int a_scale_layout, const uint8_t* b,
                       const float* b_scale, void* out, int out_dtype, int M, int N, int K,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
@@ -197,8 +199,8 @@ int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, const uint8_t* b,
  * The e8m0 scales are applied inside the MFMA (gfx950 block-scaled f8f6f4).
  * Replaces fp4_gemm (src/torchinferno/kernels/deepseek_v4_tilelang.py,
  * kernel deepseek_v4_tilelang_definitions.py:674-769).  K % 128 == 0. */
-int ti_fp4_gemm(const uint8_t* a, const float* a_scale, const uint8_t* b, const uint8_t* b_scale,
-                int b_scale_layout, void* out, int out_dtype, int M, int N, int K, void* workspace,
+int ti_fp4_gemm(const uint8_t* a, const float* a_scale, int a_scale_layout, const uint8_t* b,
+                const uint8_t* b_scale, int b_scale_layout, void* out, int out_dtype, int M, int N, int K, void* workspace,
                 size_t workspace_bytes, hipStream_t stream);
 
 /* E8M0 scales [N, K/32] -> step-major [K/128][N][4] (weight preparation, run

@@ -59,8 +59,10 @@ def test_fp4_gemm_every_kind(dev, monkeypatch, kind, splits):
     y = tb.fp4_gemm(a, a_s, b, b_s)
     assert _rel_err(y.float().cpu().numpy(), ref) <= TOL
     st = tb.fp4_scale_stepmajor(b_s.view(torch.uint8))
-    y2 = tb._fp4_gemm_raw(a, a_s, b, st, 1, 400)
+    y2 = tb._fp4_gemm_raw(a, a_s, 0, b, st, 1, 400)
     assert torch.equal(y, y2)
+    y3 = tb._fp4_gemm_raw(a, a_s.t().contiguous(), 1, b, st, 1, 400)  # step-major activation scales
+    assert torch.equal(y, y3)
 
 
 def test_fp4_scale_stepmajor_layout(dev):

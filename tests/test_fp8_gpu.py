@@ -76,6 +76,31 @@ def test_block_act_quant_bit_exact(dev, round_scale, m, k):
     assert np.array_equal(s.cpu().numpy().view(np.uint32), os_.view(np.uint32))
 
 
+@pytest.mark.parametrize("m", [1, 77, 300])
+def test_block_act_quant_stepmajor_layout(dev, m):
+    """Scale layout 1 writes the same scales transposed, [K/128, M], and the same codes."""
+    from torchinferno_amd.kernels import block_fp8 as tb
+    x = (torch.randn((m, 1024), generator=torch.Generator().manual_seed(m)) * 3).to(torch.bfloat16).to(dev)
+    y, s = tb.act_quant(x)
+    y_t, s_t = tb._act_quant_stepmajor(x)
+    assert s_t.shape == (8, m)
+    assert torch.equal(y.view(torch.uint8), y_t.view(torch.uint8))
+    assert torch.equal(s.t(), s_t)
+
+
+def test_block_linear_stepmajor_matches_public_path(dev):
+    """The DSv4 linear (step-major scales inside) equals act_quant + fp8_gemm bit for bit."""
+    from torchinferno_amd.kernels import block_fp8 as tb
+    a, a_s, b, b_s = _problem_block(1, 1024, 384, 5, dev)
+    x = (torch.randn((3, 70, 1024), generator=torch.Generator().manual_seed(2))).to(torch.bfloat16).to(dev)
+    xq, xs = tb.act_quant(x)
+    ref = tb.fp8_gemm(xq, xs, b, b_s)
+    got = tb.linear(x, b, b_s)
+    assert got.shape == (3, 70, 384) and torch.equal(got, ref)
+    empty = tb.linear(x[:, :0], b, b_s)
+    assert empty.shape == (3, 0, 384)
+
+
 def test_block_act_quant_inplace_round_trip(dev):
     from torchinferno_amd.kernels import block_fp8 as tb
     g = torch.Generator().manual_seed(5)
@@ -219,6 +244,9 @@ def test_every_tile_kind(dev, monkeypatch, kind, mode):
             out = tb.fp8_gemm(a, a_s, b, b_s)
             torch.cuda.synchronize()
             err = _check_block(out, a, a_s, b, b_s, np.random.default_rng(0), 10**9, 10**9)
+            # step-major activation scales [K/128, M]: same products, same order
+            out_t = tb._fp8_gemm_raw(a, a_s.t().contiguous(), 1, b, b_s)
+            assert torch.equal(out, out_t), (kind, splits)
         assert err <= TOL, (kind, mode, splits, err)
 
 

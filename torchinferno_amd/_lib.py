@@ -42,15 +42,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ti_w4a16_gemm": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ti_w4a16_plan_name": (_i, [_i, _i, _i, _i, ctypes.c_char_p, _sz]),
     "ti_fp8_quant_per_token": (_i, [_vp, _i, _i, _i, _f, _vp, _vp, _vp]),
-    "ti_fp8_quant_block": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
+    "ti_fp8_quant_block": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp]),
     "ti_fp8_quant_tensor": (_i, [_vp, _i, ctypes.c_long, _vp, _vp, _vp]),
     "ti_fp8_rmsnorm_quant_per_token": (_i, [_vp, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _vp]),
     "ti_fp8_swiglu_quant_per_token": (_i, [_vp, ctypes.c_long, _vp, ctypes.c_long, _i, _i, _i, _vp, _vp, _vp]),
     "ti_fp8_gemm_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "ti_fp8_gemm_workspace_bytes_max": (_sz, [_i, _i, _i, _i]),
     "ti_fp8_gemm_rowcol": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
-    "ti_fp8_gemm_block": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
-    "ti_fp4_gemm": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "ti_fp8_gemm_block": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "ti_fp4_gemm": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ti_fp4_scale_stepmajor": (_i, [_vp, _i, _i, _vp, _vp]),
     "ti_moe_route_topk": (_i, [_vp, _i, _i, _i, _i, _f, _vp, _vp, _vp]),
     "ti_fp8_moe_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),

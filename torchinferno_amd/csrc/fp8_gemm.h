@@ -31,6 +31,7 @@ struct GemmArgs {
   long b_expert_stride;     // bytes between experts' [N, K] weights
   long sb_expert_stride;    // 4-byte units between experts' weight-scale grids
   int sb_layout;            // SMODE 2: 0 = e8m0 [N, K/32]; 1 = step-major [K/128][N][4]
+  int sa_layout;            // SMODE 1/2: 0 = [M, K/128]; 1 = step-major [K/128][M]
 };
 
 struct GemmPlan {

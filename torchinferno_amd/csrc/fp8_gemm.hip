@@ -197,11 +197,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
   const uint8_t* dsrc[NI_HI];
   uint32_t dlds[NI_HI];
   bool dwide[NI_HI];
-  int dstep[NI_HI];  // source bytes per K step; 0: a 4-byte scale per 128 K
+  int dstep[NI_HI];     // source bytes per K step, or per 128 K for the scale entries
+  bool dper128[NI_HI];  // scale entry: advances every 128 K (a 64-wide step reads one twice)
 #pragma unroll
   for (int u = 0; u < NI_HI; ++u) {
     const int id = min(wave + u * W, NI - 1);
     dstep[u] = BK;
+    dper128[u] = false;
     if (id < NI_AB) {
       const bool is_a = id < A_BYTES / 1024;
       const int j = is_a ? id : id - A_BYTES / 1024;
@@ -224,10 +226,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
       const int j = id - NI_AB;
       long row = min(m0 + min(j * 64 + lane, BM - 1), Mlim - 1);
       if (x.row_index) row = x.row_index[row];
-      dsrc[u] = (const uint8_t*)(x.sa + row * KB);
+      // [M, K/128]: one scattered dword per row; step-major [K/128][M]: the
+      // tile's rows adjacent.
+      dsrc[u] = (const uint8_t*)(x.sa + (x.sa_layout ? row : row * KB));
       dlds[u] = (uint32_t)(A_BYTES + B_BYTES + j * 256);
       dwide[u] = false;
-      dstep[u] = 0;
+      dstep[u] = x.sa_layout ? M * 4 : 4;
+      dper128[u] = true;
     } else if constexpr (SMODE == 1) {
       // Only the tile's BN/128 column blocks are read; the other lanes repeat
       // the last one (one cache line per step instead of 64).
@@ -235,7 +240,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
       dsrc[u] = (const uint8_t*)(sbmat + (long)nb * KB);
       dlds[u] = (uint32_t)(A_BYTES + B_BYTES + NI_SA * 256);
       dwide[u] = false;
-      dstep[u] = 0;
+      dstep[u] = 4;
+      dper128[u] = true;
     } else {
       // e8m0 bytes, the row's dword of K step kk: [N, K/32] layout at byte
       // nrow * K/32 + 4*kk (one dword per row: scattered), step-major
@@ -256,7 +262,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
     for (int u = 0; u < NI_HI; ++u) {
       if (wave + u * W >= NI) break;
       if (dwide[u]) dma16(dsrc[u] + kk * dstep[u], base + dlds[u]);
-      else dma4(dsrc[u] + (dstep[u] ? kk * dstep[u] : (kk * BK / 128) * 4), base + dlds[u]);
+      else dma4(dsrc[u] + (dper128[u] ? (kk * BK / 128) * dstep[u] : kk * dstep[u]), base + dlds[u]);
     }
   };
 
@@ -633,7 +639,7 @@ using namespace ti::fp8;
 static int gemm_common(const char* name, int smode, const uint8_t* a, const float* a_scale,
                        int a_scale_stride, const uint8_t* b, const float* b_scale, int b_scale_stride,
                        void* out, int out_dtype, int M, int N, int K, void* workspace,
-                       size_t workspace_bytes, hipStream_t stream) {
+                       size_t workspace_bytes, hipStream_t stream, int a_scale_layout = 0) {
   TI_CHECK_ARG(a && b && a_scale && b_scale && out, "%s: null pointer", name);
   TI_CHECK_ARG(out_dtype == TI_DTYPE_BF16 || out_dtype == TI_DTYPE_F16, "%s: out dtype must be bf16 or fp16",
                name);
@@ -649,6 +655,7 @@ static int gemm_common(const char* name, int smode, const uint8_t* a, const floa
   x.a = a; x.b = b; x.sa = a_scale; x.sb = b_scale;
   x.sa_stride = a_scale_stride; x.sb_stride = b_scale_stride;
   x.sb_layout = smode == 2 ? b_scale_stride : 0;
+  x.sa_layout = smode >= 1 ? a_scale_layout : 0;
   x.out = (uint16_t*)out;
   x.M = M; x.N = N; x.K = K;
   x.splits = p.splits; x.tiles_m = p.tiles_m; x.tiles_n = p.tiles_n; x.group_m = p.group_m;
@@ -694,19 +701,21 @@ extern "C" int ti_fp8_gemm_rowcol(const uint8_t* a, const float* a_scale, int a_
                      b_scale_per_col ? 1 : 0, out, out_dtype, M, N, K, workspace, workspace_bytes, stream);
 }
 
-extern "C" int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, const uint8_t* b,
+extern "C" int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, int a_scale_layout, const uint8_t* b,
                                  const float* b_scale, void* out, int out_dtype, int M, int N, int K,
                                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  TI_CHECK_ARG(a_scale_layout == 0 || a_scale_layout == 1, "ti_fp8_gemm_block: a_scale_layout must be 0 or 1");
   return gemm_common("ti_fp8_gemm_block", 1, a, a_scale, 0, b, b_scale, 0, out, out_dtype, M, N, K, workspace,
-                     workspace_bytes, stream);
+                     workspace_bytes, stream, a_scale_layout);
 }
 
-extern "C" int ti_fp4_gemm(const uint8_t* a, const float* a_scale, const uint8_t* b, const uint8_t* b_scale,
-                           int b_scale_layout, void* out, int out_dtype, int M, int N, int K, void* workspace,
-                           size_t workspace_bytes, hipStream_t stream) {
+extern "C" int ti_fp4_gemm(const uint8_t* a, const float* a_scale, int a_scale_layout, const uint8_t* b,
+                           const uint8_t* b_scale, int b_scale_layout, void* out, int out_dtype, int M, int N, int K,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  TI_CHECK_ARG(a_scale_layout == 0 || a_scale_layout == 1, "ti_fp4_gemm: a_scale_layout must be 0 or 1");
   TI_CHECK_ARG(b_scale_layout == 0 || b_scale_layout == 1, "ti_fp4_gemm: b_scale_layout must be 0 or 1");
   return gemm_common("ti_fp4_gemm", 2, a, a_scale, 0, b, (const float*)b_scale, b_scale_layout, out, out_dtype, M,
-                     N, K, workspace, workspace_bytes, stream);
+                     N, K, workspace, workspace_bytes, stream, a_scale_layout);
 }
 
 namespace {

@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256) void quant_per_token_kernel(const uint16_t* __
 template <int DT, bool POW2>
 __global__ __launch_bounds__(256) void quant_block_kernel(const uint16_t* __restrict__ x, int M, int K,
                                                           uint8_t* __restrict__ q,
-                                                          float* __restrict__ s) {
+                                                          float* __restrict__ s, int s_layout) {
   const int lane = threadIdx.x & 63;
   const int KB = K / 128;
   const long blk = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256) void quant_block_kernel(const uint16_t* __rest
   const float y0 = fminf(fmaxf(f0 / sc, -kE4M3Max), kE4M3Max);
   const float y1 = fminf(fmaxf(f1 / sc, -kE4M3Max), kE4M3Max);
   *(uint16_t*)(q + off) = (uint16_t)(e4m3_encode(y0) | (e4m3_encode(y1) << 8));
-  if (lane == 0) s[row * KB + kb] = sc;
+  if (lane == 0) s[s_layout ? (long)kb * M + row : row * KB + kb] = sc;
 }
 
 // q = e4m3(x * inv_scale[0]); n % 8 == 0.
@@ -304,10 +304,12 @@ extern "C" int ti_fp8_quant_per_token(const void* x, int x_dtype, int M, int K, 
 }
 
 extern "C" int ti_fp8_quant_block(const void* x, int x_dtype, int M, int K, int block_size,
-                                  int round_scale, uint8_t* xq, float* xs, hipStream_t stream) {
+                                  int round_scale, uint8_t* xq, float* xs, int scale_layout,
+                                  hipStream_t stream) {
   TI_CHECK_ARG(x && xq && xs, "ti_fp8_quant_block: null pointer");
   TI_CHECK_ARG(act_dtype_ok(x_dtype), "ti_fp8_quant_block: x must be fp16 or bf16");
   TI_CHECK_SHAPE(block_size == 128, "ti_fp8_quant_block: block_size must be 128 (got %d)", block_size);
+  TI_CHECK_ARG(scale_layout == 0 || scale_layout == 1, "ti_fp8_quant_block: scale_layout must be 0 or 1");
   TI_CHECK_SHAPE(M >= 0 && K > 0 && K % 128 == 0, "ti_fp8_quant_block: need K %% 128 == 0 (K=%d)", K);
   TI_CHECK_ARG(((uintptr_t)x & 3) == 0 && ((uintptr_t)xq & 1) == 0,
                "ti_fp8_quant_block: x must be 4-byte and xq 2-byte aligned");
@@ -316,7 +318,7 @@ extern "C" int ti_fp8_quant_block(const void* x, int x_dtype, int M, int K, int 
   dim3 grid((unsigned)((blocks + 3) / 4));
 #define TI_QB(DT, P2)                                                                             \
   hipLaunchKernelGGL((quant_block_kernel<DT, P2>), grid, dim3(256), 0, stream, (const uint16_t*)x, \
-                     M, K, xq, xs)
+                     M, K, xq, xs, scale_layout)
   if (x_dtype == TI_DTYPE_F16) {
     if (round_scale) TI_QB(TI_DTYPE_F16, true); else TI_QB(TI_DTYPE_F16, false);
   } else {

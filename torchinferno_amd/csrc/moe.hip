@@ -351,7 +351,7 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
   const bool f4 = smode == 2;
 
   // 1. hidden -> e4m3 1x128
-  int st = ti_fp8_quant_block(hidden, TI_DTYPE_BF16, T, H, 128, 0, w.xq, w.xs, stream);
+  int st = ti_fp8_quant_block(hidden, TI_DTYPE_BF16, T, H, 128, 0, w.xq, w.xs, 0, stream);
   if (st != TI_OK) return st;
   // 2. align
   hipLaunchKernelGGL(align_kernel, dim3(1), dim3(kAlignThreads), 0, stream, (const int*)topk_ids, (int)R, E, p.bm,

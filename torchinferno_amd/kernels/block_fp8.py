@@ -51,7 +51,7 @@ def act_quant(
     y = torch.empty(value.shape, dtype=FP8_E4M3, device=x.device)
     s = torch.empty((*value.shape[:-1], n // block_size), dtype=torch.float32, device=x.device)
     _lib.call("ti_fp8_quant_block", value.data_ptr(), _lib.dtype_code(value.dtype), rows, n, block_size,
-              int(scale_fmt is not None), y.data_ptr(), s.data_ptr(), _lib.stream_of(value))
+              int(scale_fmt is not None), y.data_ptr(), s.data_ptr(), 0, _lib.stream_of(value))
     if inplace:
         deq = y.view(rows, n // block_size, block_size).float() * s.view(rows, -1, 1)
         x.copy_(deq.view(x.shape).to(x.dtype))
@@ -84,11 +84,39 @@ def fp8_gemm(
         raise ValueError("FP8 GEMM weight must be [N, K] with the activation's K")
     if a_s.numel() != m * (k // BLOCK) or tuple(b_s.shape) != (-(-n // BLOCK), -(-k // BLOCK)):
         raise ValueError("FP8 GEMM block scales must be a_s [M, K/128] and b_s [ceil(N/128), K/128]")
+    return _fp8_gemm_raw(a, a_s, 0, b, b_s)
+
+
+def _fp8_gemm_raw(a: Tensor, a_s: Tensor, a_layout: int, b: Tensor, b_s: Tensor) -> Tensor:
+    k = a.size(-1)
+    m = a.numel() // k
+    n = b.size(0)
     out = torch.empty((*a.shape[:-1], n), dtype=torch.bfloat16, device=a.device)
+    if m == 0:
+        return out
     ws, ws_bytes = _ws_args(a.device, m, n, k, 1)
-    _lib.call("ti_fp8_gemm_block", a.data_ptr(), a_s.data_ptr(), b.data_ptr(), b_s.data_ptr(), out.data_ptr(),
-              _lib.TI_DTYPE_BF16, m, n, k, ws, ws_bytes, _lib.stream_of(a))
+    _lib.call("ti_fp8_gemm_block", a.data_ptr(), a_s.data_ptr(), a_layout, b.data_ptr(), b_s.data_ptr(),
+              out.data_ptr(), _lib.TI_DTYPE_BF16, m, n, k, ws, ws_bytes, _lib.stream_of(a))
     return out
+
+
+def _act_quant_stepmajor(x: Tensor) -> tuple[Tensor, Tensor]:
+    """1x128 quant with the scales step-major, ``[K/128, rows]`` (the layout the
+    GEMMs read as one contiguous run per tile and K step)."""
+    _lib.require_device(x)
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("FP8 block quantization input must be bf16 or fp16")
+    n = x.size(-1)
+    if n % BLOCK:
+        raise ValueError("FP8 quantization width must be divisible by block size")
+    value = x.contiguous()
+    rows = value.numel() // n
+    y = torch.empty(value.shape, dtype=FP8_E4M3, device=x.device)
+    s = torch.empty((n // BLOCK, rows), dtype=torch.float32, device=x.device)
+    if rows:
+        _lib.call("ti_fp8_quant_block", value.data_ptr(), _lib.dtype_code(value.dtype), rows, n, BLOCK, 0,
+                  y.data_ptr(), s.data_ptr(), 1, _lib.stream_of(value))
+    return y, s
 
 
 FP4 = torch.float4_e2m1fn_x2
@@ -124,12 +152,15 @@ def fp4_scale_stepmajor(scale_bytes: Tensor) -> Tensor:
     return dst.view(*lead, kb // 4, n, 4)
 
 
-def _fp4_gemm_raw(a: Tensor, a_s: Tensor, b: Tensor, eb: Tensor, layout: int, n: int) -> Tensor:
+def _fp4_gemm_raw(a: Tensor, a_s: Tensor, a_layout: int, b: Tensor, eb: Tensor, layout: int, n: int) -> Tensor:
     k = a.size(-1)
     m = a.numel() // k
     out = torch.empty((*a.shape[:-1], n), dtype=torch.bfloat16, device=a.device)
+    if m == 0:
+        return out
     ws, ws_bytes = _ws_args(a.device, m, n, k, 2)
-    _lib.call("ti_fp4_gemm", a.data_ptr(), a_s.data_ptr(), b.data_ptr(), eb.data_ptr(), layout, out.data_ptr(),
+    _lib.call("ti_fp4_gemm", a.data_ptr(), a_s.data_ptr(), a_layout, b.data_ptr(), eb.data_ptr(), layout,
+              out.data_ptr(),
               _lib.TI_DTYPE_BF16, m, n, k, ws, ws_bytes, _lib.stream_of(a))
     return out
 
@@ -162,14 +193,14 @@ def fp4_gemm(
     eb = e8m0_bytes(b_s)
     if a_s.numel() != m * (k // BLOCK) or tuple(eb.shape) != (n, k // 32):
         raise ValueError("FP4 GEMM scales must be a_s [M, K/128] and b_s [N, K/32]")
-    return _fp4_gemm_raw(a, a_s, b, eb, 0, n)
+    return _fp4_gemm_raw(a, a_s, 0, b, eb, 0, n)
 
 
 def linear(x: Tensor, weight: Tensor, weight_scale: Tensor) -> Tensor:
     """DeepSeek ``linear`` for an e4m3 or MXFP4 weight (src/torchinferno/models/
     deepseek_v4/tensor_parallel.py:195-207): ``act_quant`` then ``fp8_gemm`` /
-    ``fp4_gemm``, bf16 out."""
-    xq, xs = act_quant(x)
+    ``fp4_gemm``, bf16 out.  The activation scales stay internal, so they are
+    kept step-major (``[K/128, rows]``), which the GEMMs read fastest."""
     if weight.dtype == FP4:
         # The step-major copy of the weight's scales is built on first use and
         # cached on the weight (like the reference's per-layer weight caches).
@@ -180,7 +211,18 @@ def linear(x: Tensor, weight: Tensor, weight_scale: Tensor) -> Tensor:
                 raise ValueError("MXFP4 weight scale must be [N, K/32]")
             cached = (weight_scale, fp4_scale_stepmajor(eb))
             weight._ti_fp4_scale_stepmajor = cached
-        if xq.size(-1) != weight.size(1) * 2:
+        if x.size(-1) != weight.size(1) * 2:
             raise ValueError("MXFP4 weight K does not match the activation")
-        return _fp4_gemm_raw(xq.contiguous(), xs.contiguous(), weight, cached[1], 1, weight.size(0))
-    return fp8_gemm(xq, xs, weight, weight_scale)
+        xq, xs = _act_quant_stepmajor(x)
+        return _fp4_gemm_raw(xq, xs, 1, weight, cached[1], 1, weight.size(0))
+    if weight.dtype != FP8_E4M3 or weight_scale.dtype != torch.float32:
+        raise ValueError("block-FP8 linear needs a float8_e4m3fn weight with fp32 block scales")
+    k = x.size(-1)
+    n = weight.size(0)
+    if weight.ndim != 2 or weight.size(1) != k:
+        raise ValueError("FP8 GEMM weight must be [N, K] with the activation's K")
+    if tuple(weight_scale.shape) != (-(-n // BLOCK), -(-k // BLOCK)):
+        raise ValueError("FP8 GEMM weight scale must be [ceil(N/128), K/128]")
+    _lib.require_device(weight, weight_scale)
+    xq, xs = _act_quant_stepmajor(x)
+    return _fp8_gemm_raw(xq, xs, 1, weight.contiguous(), weight_scale.contiguous())
