@@ -42,6 +42,26 @@ __device__ __forceinline__ i32x4 unpack8(uint32_t w, uint32_t mask, uint32_t mag
   return r;
 }
 
+// Two words at once: one 64-bit shift yields both words' shifted copies (the
+// low word's top bits pick up the high word's low nibbles, which the mask
+// discards), so a pair costs 3 shifts instead of 6.
+__device__ __forceinline__ void unpack16(uint32_t w0, uint32_t w1, uint32_t mask, uint32_t magic, i32x4& r0,
+                                         i32x4& r1) {
+  const uint64_t x = ((uint64_t)w1 << 32) | w0;
+  uint64_t s4, s8, s12;
+  asm("v_lshrrev_b64 %0, 4, %1" : "=v"(s4) : "v"(x));
+  asm("v_lshrrev_b64 %0, 8, %1" : "=v"(s8) : "v"(x));
+  asm("v_lshrrev_b64 %0, 12, %1" : "=v"(s12) : "v"(x));
+  r0[0] = (int)and_or(w0, mask, magic);
+  r0[1] = (int)and_or((uint32_t)s4, mask, magic);
+  r0[2] = (int)and_or((uint32_t)s8, mask, magic);
+  r0[3] = (int)and_or((uint32_t)s12, mask, magic);
+  r1[0] = (int)and_or(w1, mask, magic);
+  r1[1] = (int)and_or((uint32_t)(s4 >> 32), mask, magic);
+  r1[2] = (int)and_or((uint32_t)(s8 >> 32), mask, magic);
+  r1[3] = (int)and_or((uint32_t)(s12 >> 32), mask, magic);
+}
+
 template <int DT>
 __device__ __forceinline__ f32x4 mfma16x16x32(i32x4 a, i32x4 b, f32x4 c) {
   if constexpr (DT == TI_DTYPE_F16) {
@@ -73,9 +93,12 @@ __device__ __forceinline__ void compute_group(const i32x4 (&w)[NT], const i32x4 
   }
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
+    // The 64-bit-shift unpack: measured 1-4% faster in the skinny kernels
+    // (M <= 32); the tall-tile compute below keeps the 32-bit form, where it
+    // measured neutral to slightly slower.
     i32x4 b[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = unpack8<DT>((uint32_t)w[t][j], mask, magic);
+    unpack16((uint32_t)w[t][0], (uint32_t)w[t][1], mask, magic, b[0], b[1]);
+    unpack16((uint32_t)w[t][2], (uint32_t)w[t][3], mask, magic, b[2], b[3]);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       f32x4 cc = nbias[mt];
