@@ -277,6 +277,34 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int e = 0; e < MM::NACC; ++e) acc[i][j][e] = 0.f;
+  // Scaled modes fold each step's partial sums into acc with a per-row scale.
+  // Small wave tiles defer that fold by one step: the fold of step i-1 runs
+  // while step i's MFMAs execute, instead of waiting on their result (with
+  // one wave per SIMD nothing else hides that latency).  Same products and
+  // association, so the same results.  pd/sd: the deferred partials and
+  // scales (zero before the first step: acc + 0*0 = acc).
+  constexpr bool DEFER = SMODE >= 1 && FM * FN * MM::NACC <= 32;
+  acc_t pd[DEFER ? FM : 1][DEFER ? FN : 1];
+  float sd[DEFER ? FM : 1][MM::NACC];
+#pragma unroll
+  for (int i = 0; i < (DEFER ? FM : 1); ++i) {
+#pragma unroll
+    for (int e = 0; e < MM::NACC; ++e) sd[i][e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < (DEFER ? FN : 1); ++j)
+#pragma unroll
+      for (int e = 0; e < MM::NACC; ++e) pd[i][j][e] = 0.f;
+  }
+  auto fold = [&](int fm, int fn, const acc_t& p, const float (&srow)[MM::NACC]) {
+    if constexpr (DEFER) {
+#pragma unroll
+      for (int e = 0; e < MM::NACC; ++e) acc[fm][fn][e] = __builtin_fmaf(pd[fm][fn][e], sd[fm][e], acc[fm][fn][e]);
+      pd[fm][fn] = p;
+    } else {
+#pragma unroll
+      for (int e = 0; e < MM::NACC; ++e) acc[fm][fn][e] = __builtin_fmaf(p[e], srow[e], acc[fm][fn][e]);
+    }
+  };
 
   const int arow0 = wm * TM + (lane % MF);
   const int brow0 = wn * TN + (lane % MF);
@@ -360,8 +388,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
           for (int e = 0; e < MM::NACC; ++e) p[e] = 0.f;
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) p = MM::mma4(af[ks], bf[ks][fn], p, eb[ks][fn]);
+          fold(fm, fn, p, srow);
+        }
+        if constexpr (DEFER) {
 #pragma unroll
-          for (int e = 0; e < MM::NACC; ++e) acc[fm][fn][e] = __builtin_fmaf(p[e], srow[e], acc[fm][fn][e]);
+          for (int e = 0; e < MM::NACC; ++e) sd[fm][e] = srow[e];
         }
       }
     } else {
@@ -402,11 +433,22 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
           for (int e = 0; e < MM::NACC; ++e) p[e] = 0.f;
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) p = MM::mma(af[ks], bf[ks][fn], p);
+          fold(fm, fn, p, srow);
+        }
+        if constexpr (DEFER) {
 #pragma unroll
-          for (int e = 0; e < MM::NACC; ++e) acc[fm][fn][e] = __builtin_fmaf(p[e], srow[e], acc[fm][fn][e]);
+          for (int e = 0; e < MM::NACC; ++e) sd[fm][e] = srow[e];
         }
       }
     }
+  }
+  if constexpr (DEFER) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int e = 0; e < MM::NACC; ++e) acc[fm][fn][e] = __builtin_fmaf(pd[fm][fn][e], sd[fm][e], acc[fm][fn][e]);
   }
   wait_vm_all();
 
@@ -518,6 +560,10 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
       case 5: launch_cfg<64, 128, 128, 1, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
       case 6: launch_cfg<16, 128, 128, 1, 4, 16, 6, SMODE, ODT>(p, x, stream); break;
       case 9: launch_cfg<256, 128, 128, 4, 2, 32, 3, SMODE, ODT>(p, x, stream); break;
+      case 10: launch_cfg<16, 256, 128, 1, 8, 16, 4, SMODE, ODT>(p, x, stream); break;
+      case 11: launch_cfg<16, 128, 128, 1, 8, 16, 6, SMODE, ODT>(p, x, stream); break;
+      case 12: launch_cfg<32, 128, 128, 1, 8, 16, 6, SMODE, ODT>(p, x, stream); break;
+      case 13: launch_cfg<64, 128, 128, 2, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
       default: launch_cfg<256, 256, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
     }
   } else {
@@ -531,13 +577,17 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
       case 6: launch_cfg<16, 128, 128, 1, 4, 16, 6, SMODE, ODT>(p, x, stream); break;
       case 7: launch_cfg<128, 128, 64, 2, 2, 32, 6, SMODE, ODT>(p, x, stream); break;
       case 8: launch_cfg<256, 128, 64, 2, 2, 32, 6, SMODE, ODT>(p, x, stream); break;
+      case 10: launch_cfg<16, 256, 128, 1, 8, 16, 4, SMODE, ODT>(p, x, stream); break;
+      case 11: launch_cfg<16, 128, 128, 1, 8, 16, 6, SMODE, ODT>(p, x, stream); break;
+      case 12: launch_cfg<32, 128, 128, 1, 8, 16, 6, SMODE, ODT>(p, x, stream); break;
+      case 13: launch_cfg<64, 128, 128, 2, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
       default: launch_cfg<256, 128, 128, 4, 2, 32, 3, SMODE, ODT>(p, x, stream); break;
     }
   }
 }
 
-const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256};
-const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128, 128, 128, 128};
+const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256, 16, 16, 32, 64};
+const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128, 128, 128, 128, 256, 128, 128, 128};
 
 int env_int(const char* name, int dflt) {
   const char* e = getenv(name);
@@ -550,26 +600,56 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   GemmPlan p;
   const int KT = K / 128;
   // Measured on MI355X at the Llama-3-70B / DeepSeek-V3 shapes (BASELINE
-  // configs 2 and 3): skinny M streams B with 16- or 64-row tiles, split over K
-  // when too few column tiles cover the 256 CUs; larger M takes the largest
-  // tile that still gives every CU a workgroup (256x256, then 256x128 -- block
-  // scales favour it from 128 tiles -- then 128x128, split over K below 128).
+  // configs 2 and 3): skinny M streams B with 16- to 64-row tiles, split over
+  // K when too few column tiles cover the 256 CUs; larger M takes the largest
+  // tile that still gives every CU a workgroup (256x256, then 256x128 from 144
+  // tiles -- 128 with block or MXFP4 scales -- then 128x128, split over K
+  // below 128).
   auto tiles = [&](int bm, int bn) { return (long)cdiv(M, bm) * cdiv(N, bn); };
   int splits = 1;
   if (M <= 4) {
     p.kind = 3;
     const long t = tiles(16, 256);
     splits = t >= 128 ? 1 : (int)(cdiv(256, (int)t) < 4 ? cdiv(256, (int)t) : 4);
-  } else if (M <= 64) {
-    p.kind = M <= 16 ? 6 : 5;
-    const long t = tiles(kBM[p.kind], kBN[p.kind]);
+  } else if (M <= 16) {
+    // 8-wave 16x128 tiles: two waves per SIMD hide each other's per-step
+    // LDS/MFMA latency (12-24% faster than the 4-wave tile at M=16).
+    p.kind = 11;
+    const long t = tiles(16, 128);
     splits = t >= 72 ? 1 : (int)(cdiv(256, (int)t) < 4 ? cdiv(256, (int)t) : 4);
+  } else if (M <= 32) {
+    p.kind = 12;
+    splits = tiles(32, 128) >= 128 ? 1 : 2;
+  } else if (M <= 64) {
+    // Measured per scale mode at the config-2/3 shapes: 64x128 8-wave tiles
+    // when they alone fill the CUs, else 32x128 (per-token FP8 and MXFP4) or
+    // 64x128 split over K (block FP8); deep K (>= 16384) prefers fewer splits.
+    const bool deep = K >= 16384;
+    if (tiles(64, 128) >= 128) {
+      p.kind = 13;
+    } else if (smode == 0) {
+      p.kind = deep ? 13 : 12;
+      splits = deep ? 4 : 1;
+    } else if (smode == 1) {
+      p.kind = 13;
+      splits = deep ? 1 : 2;
+    } else {
+      p.kind = 12;
+      splits = deep ? 1 : 2;
+    }
   } else if (M <= 128) {
-    p.kind = 5;
-    splits = tiles(64, 128) >= 128 ? 1 : 2;
+    // 128x128 tiles when they fill the CUs (per-token and block FP8), else
+    // 8-wave 64x128, split over K when fewer than 160 tiles (4 ways for
+    // MXFP4 at deep K).
+    if (smode != 2 && tiles(128, 128) >= 128) {
+      p.kind = 2;
+    } else {
+      p.kind = 13;
+      splits = tiles(64, 128) >= 160 ? 1 : ((smode == 2 && K >= 16384) ? 4 : 2);
+    }
   } else if (tiles(256, 256) >= 256) {
     p.kind = 1;
-  } else if (tiles(256, 128) >= (smode >= 1 ? 128 : 256)) {
+  } else if (tiles(256, 128) >= (smode >= 1 ? 128 : 144)) {
     p.kind = 9;
   } else {
     p.kind = 2;
@@ -597,6 +677,9 @@ void launch_grouped_smode(int kind, const GemmArgs& x, int max_mtiles, hipStream
     case 2: launch_grouped_cfg<128, 128, 128, 2, 2, 32, 3, SMODE>(x, max_mtiles, stream); break;
     case 5: launch_grouped_cfg<64, 128, 128, 1, 4, 16, 4, SMODE>(x, max_mtiles, stream); break;
     case 9: launch_grouped_cfg<256, 128, 128, 4, 2, 32, 3, SMODE>(x, max_mtiles, stream); break;
+    case 11: launch_grouped_cfg<16, 128, 128, 1, 8, 16, 6, SMODE>(x, max_mtiles, stream); break;
+    case 12: launch_grouped_cfg<32, 128, 128, 1, 8, 16, 6, SMODE>(x, max_mtiles, stream); break;
+    case 13: launch_grouped_cfg<64, 128, 128, 2, 4, 16, 4, SMODE>(x, max_mtiles, stream); break;
     default: launch_grouped_cfg<16, 128, 128, 1, 4, 16, 6, SMODE>(x, max_mtiles, stream); break;
   }
 }

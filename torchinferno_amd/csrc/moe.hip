@@ -120,11 +120,13 @@ Plan make_plan(int T, int k, int E) {
   const long R = (long)T * k;
   const long avg = (R + E - 1) / E;
   Plan p;
-  p.kind = avg <= 16 ? 6 : (avg <= 48 ? 5 : (avg <= 160 ? 2 : 9));
+  // Measured at the config-4 shapes: 8-wave 16- / 32-row tiles for few rows
+  // per expert (T=64: avg 2; T=512: avg 16), 128x128 around avg 128.
+  p.kind = avg <= 8 ? 11 : (avg <= 48 ? 12 : (avg <= 160 ? 2 : 9));
   const char* env = getenv("TI_ROCM_MOE_KIND");
   if (env && *env) {
     const int kk = atoi(env);
-    if (kk == 2 || kk == 5 || kk == 6 || kk == 9) p.kind = kk;
+    if (kk == 2 || kk == 5 || kk == 6 || kk == 9 || kk == 11 || kk == 12 || kk == 13) p.kind = kk;
   }
   p.bm = fp8::grouped_bm(p.kind);
   p.max_tiles = (int)(R / p.bm + E + 1);
