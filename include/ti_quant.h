@@ -182,7 +182,9 @@ int ti_fp8_gemm_rowcol(const uint8_t* a, const float* a_scale, int a_scale_per_r
                        void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Block-scaled: out[m,n] = sum_kb (a . b^T over K block kb) * a_scale[m,kb] *
- * b_scale[n/128, kb]; a_scale [M, K/128], b_scale [ceil(N/128), K/128], fp32.
+ * b_scale[n/128, kb]; b_scale [ceil(N/128), K/128] fp32; a_scale fp32
+ * [M, K/128] for a_scale_layout 0 (the reference's), step-major [K/128, M]
+ * for 1 (one contiguous read per tile and K step; ti_fp8_quant_block writes it).
  * Replaces fp8_gemm (src/torchinferno/kernels/deepseek_v4_tilelang.py:207-223,
  * kernel deepseek_v4_tilelang_definitions.py:436-485). */
 int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, int a_scale_layout, const uint8_t* b,
@@ -191,7 +193,7 @@ int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, int a_scale_layout
 
 /* FP8 activations x MXFP4 weights: out[m,n] = sum_k a[m,k] * a_scale[m, k/128]
  * * w[n,k] * 2^(e[n, k/32] - 127).  a e4m3 [M,K] with fp32 1x128 scales
- * [M, K/128]; b e2m1 [N, K/2] (two values per byte along K, element 2i in the
+ * ([M, K/128] for a_scale_layout 0, step-major [K/128, M] for 1); b e2m1 [N, K/2] (two values per byte along K, element 2i in the
  * low nibble -- torch float4_e2m1fn_x2); b_scale E8M0 bytes, layout 0 = the
  * checkpoint's [N, K/32], layout 1 = step-major [K/128][N][4] (the 4 scales
  * of a 128-wide K step of each row adjacent to the next row's, so a tile's
