@@ -312,10 +312,27 @@ void launch_eight(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) 
   }
 }
 
+// 16-wave workgroups (four waves per SIMD), the configurations of kSixteen.
+template <int DT>
+void launch_sixteen(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
+  if (p.mr == 64) launch_split<DT, 64, 2, 2, 2, 16>(p, x, stream);
+  else if (p.mr == 32) {
+    if (p.nt == 2) launch_split<DT, 32, 2, 4, 2, 16>(p, x, stream);
+    else launch_split<DT, 32, 1, 4, 3, 16>(p, x, stream);
+  } else {
+    if (p.nt == 2) launch_split<DT, 16, 2, 4, 3, 16>(p, x, stream);
+    else launch_split<DT, 16, 1, 4, 4, 16>(p, x, stream);
+  }
+}
+
 template <int DT>
 void launch_mr(const DecodePlan& p, const DecodeArgs& x, hipStream_t stream) {
   if (p.waves == 8) {
     launch_eight<DT>(p, x, stream);
+    return;
+  }
+  if (p.waves == 16) {
+    launch_sixteen<DT>(p, x, stream);
     return;
   }
   if (p.mr == 4) launch_nt<DT, 4>(p, x, stream);
@@ -336,10 +353,23 @@ constexpr EightCfg kEight[] = {{64, 4, 2, 2}, {64, 2, 2, 2}, {64, 2, 2, 3}, {32,
                                {32, 2, 2, 3}, {32, 2, 4, 3}, {32, 1, 4, 3}, {16, 4, 2, 3},
                                {16, 2, 2, 4}, {16, 2, 4, 4}, {16, 1, 4, 6}};
 
+// The instantiated 16-wave configurations.
+constexpr EightCfg kSixteen[] = {{64, 2, 2, 2}, {32, 2, 4, 2}, {32, 1, 4, 3}, {16, 2, 4, 3}, {16, 1, 4, 4}};
+
 bool eight_instantiated(const DecodePlan& p) {
+  if (p.waves == 16) {
+    for (const EightCfg& c : kSixteen)
+      if (c.mr == p.mr && c.nt == p.nt && c.wk == p.wk && c.ring == p.ring) return true;
+    return false;
+  }
   for (const EightCfg& c : kEight)
     if (c.mr == p.mr && c.nt == p.nt && c.wk == p.wk && c.ring == p.ring) return true;
   return false;
+}
+
+bool env_plan_set() {
+  const char* e = getenv("TI_ROCM_W4A16_DECODE_PLAN");
+  return e && *e;
 }
 
 // TI_ROCM_W4A16_DECODE_PLAN="nt:wk:ring:splits" overrides the heuristic (tuning).
@@ -355,16 +385,22 @@ bool env_plan(DecodePlan& p) {
 // Completes a plan: snaps (nt, wk, ring) to an instantiated configuration,
 // tiles N, caps splits and sizes the LDS (ring, staged scales, WK reduction).
 DecodePlan finish_decode_plan(DecodePlan p, int N, int NG, bool tall) {
-  if (p.waves == 8) {
-    // Snap to a kEight entry of this mr: the requested (nt, wk) if listed
+  if (p.waves == 8 || p.waves == 16) {
+    // Snap to a table entry of this mr: the requested (nt, wk) if listed
     // (its ring), else the first whose columns tile N; none -> 4 waves.
+    const EightCfg* tb = p.waves == 16 ? kSixteen : kEight;
+    const int nc = p.waves == 16 ? (int)(sizeof(kSixteen) / sizeof(kSixteen[0]))
+                                 : (int)(sizeof(kEight) / sizeof(kEight[0]));
+    const int wv = p.waves;
     const EightCfg* pick = nullptr;
-    for (const EightCfg& c : kEight)
-      if (c.mr == p.mr && c.nt == p.nt && c.wk == p.wk && N % (8 / c.wk * c.nt * 16) == 0 &&
+    for (int i = 0; i < nc; ++i) {
+      const EightCfg& c = tb[i];
+      if (c.mr == p.mr && c.nt == p.nt && c.wk == p.wk && N % (wv / c.wk * c.nt * 16) == 0 &&
           (!pick || c.ring == p.ring))
         pick = &c;
-    for (const EightCfg& c : kEight)
-      if (!pick && c.mr == p.mr && N % (8 / c.wk * c.nt * 16) == 0) pick = &c;
+    }
+    for (int i = 0; i < nc; ++i)
+      if (!pick && tb[i].mr == p.mr && N % (wv / tb[i].wk * tb[i].nt * 16) == 0) pick = &tb[i];
     if (pick) {
       p.nt = pick->nt; p.wk = pick->wk; p.ring = pick->ring;
     } else {
@@ -372,7 +408,7 @@ DecodePlan finish_decode_plan(DecodePlan p, int N, int NG, bool tall) {
       p.wk = 1;
     }
   }
-  if (p.waves == 8) {
+  if (p.waves >= 8) {
     // fixed by the table entry
   } else if (tall) {
     // The instantiated tall configurations: (2,2,2), (4,1,2|3), (2,1,2|3|4); a
@@ -395,7 +431,7 @@ DecodePlan finish_decode_plan(DecodePlan p, int N, int NG, bool tall) {
   const int wc = p.waves / p.wk * p.nt * 16;
   const int sbytes = cdiv(ngr * wc * 2, 256) * 256;
   auto fits = [&](int r) { return r * stage_bytes(p.mr, p.nt, p.wk, p.waves) + sbytes <= kDecodeLdsMax; };
-  if (p.waves == 8) {
+  if (p.waves >= 8) {
     // the table's ring; an oversized plan is stepped down by the caller
   } else if (tall) {
     while (p.ring > 2 && !fits(p.ring)) p.ring = p.ring == 4 ? 3 : 2;
@@ -429,7 +465,7 @@ DecodePlan make_decode_plan(int M, int N, int K) {
   // 32- and 64-row tiles run on 8 waves (two per SIMD, the K range split
   // between them): one wave per SIMD serializes its VALU unpack, MFMAs and LDS
   // waits.  Measured 7-19% faster than the best 4-wave plans at the
-  // Llama-3-8B MLP shapes (M = 32..128).
+  // Llama-3-8B MLP shapes (M = 32..128); some 32-row plans take 16 (below).
   p.waves = ((p.mr == 64 && wide) || p.mr == 32 || p.mr == 16) ? 8 : kWaves;
   const int NG = K / kGroup;
   if (!env_plan(p)) {
@@ -462,17 +498,25 @@ DecodePlan make_decode_plan(int M, int N, int K) {
       p.splits = (M <= 32 && blocks * p.mchunks < 256) ? 2 : 1;
     }
   }
+  // 32-row tiles at wide N, and at narrow N beyond 64 rows, measured 4-8%
+  // faster on 16 waves (four per SIMD: 64 columns x a quarter of K each).
+  if (!env_plan_set() && p.mr == 32 && (wide || M > 64)) {
+    p.waves = 16; p.nt = 2; p.wk = 4; p.ring = 2;
+  }
   const char* ew = getenv("TI_ROCM_W4A16_DECODE_WAVES");
-  if (ew && *ew && (p.mr == 16 || p.mr == 32 || p.mr == 64)) p.waves = atoi(ew) == 8 ? 8 : kWaves;
+  if (ew && *ew && (p.mr == 16 || p.mr == 32 || p.mr == 64)) {
+    const int v = atoi(ew);
+    p.waves = (v == 8 || v == 16) ? v : kWaves;
+  }
   DecodePlan q = finish_decode_plan(p, N, NG, tall);
   // An 8-wave plan whose LDS (ring + the staged scale slab, which grows with
   // K) does not fit steps down to half the columns, then to the 4-wave table.
-  if (q.waves == 8 && q.lds > kDecodeLdsMax && q.nt >= 2) {
+  if (q.waves >= 8 && q.lds > kDecodeLdsMax && q.nt >= 2) {
     p.nt = q.nt / 2;
     p.wk = q.wk;
     q = finish_decode_plan(p, N, NG, tall);
   }
-  if (q.waves == 8 && q.lds > kDecodeLdsMax) {
+  if (q.waves >= 8 && q.lds > kDecodeLdsMax) {
     p.waves = kWaves;
     p.wk = 1;
     q = finish_decode_plan(p, N, NG, tall);
@@ -481,10 +525,10 @@ DecodePlan make_decode_plan(int M, int N, int K) {
 }
 
 bool decode_plan_valid(const DecodePlan& p, int N) {
-  if (p.waves != 4 && p.waves != 8) return false;
+  if (p.waves != 4 && p.waves != 8 && p.waves != 16) return false;
   if (N % (p.waves / p.wk * p.nt * 16) || p.nblocks * (p.waves / p.wk * p.nt * 16) != N) return false;
   if (p.lds > kDecodeLdsMax) return false;
-  if (p.waves == 8) return eight_instantiated(p);
+  if (p.waves >= 8) return eight_instantiated(p);
   if (p.mr >= 64)
     return (p.nt == 2 && p.wk == 2 && p.ring == 2) || (p.nt == 4 && p.wk == 1 && (p.ring == 2 || p.ring == 3)) ||
            (p.nt == 2 && p.wk == 1 && (p.ring >= 2 && p.ring <= 4));
