@@ -564,6 +564,7 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
       case 11: launch_cfg<16, 128, 128, 1, 8, 16, 6, SMODE, ODT>(p, x, stream); break;
       case 12: launch_cfg<32, 128, 128, 1, 8, 16, 6, SMODE, ODT>(p, x, stream); break;
       case 13: launch_cfg<64, 128, 128, 2, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
+      case 15: launch_cfg<128, 128, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
       default: launch_cfg<256, 256, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
     }
   } else {
@@ -581,6 +582,7 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
       case 11: launch_cfg<16, 128, 128, 1, 8, 16, 6, SMODE, ODT>(p, x, stream); break;
       case 12: launch_cfg<32, 128, 128, 1, 8, 16, 6, SMODE, ODT>(p, x, stream); break;
       case 13: launch_cfg<64, 128, 128, 2, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
+      case 15: launch_cfg<128, 128, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
       case 14:
         if constexpr (SMODE == 0) launch_cfg<256, 256, 128, 4, 4, 32, 2, SMODE, ODT>(p, x, stream);
         break;
@@ -589,8 +591,8 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
   }
 }
 
-const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256, 16, 16, 32, 64, 256};
-const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128, 128, 128, 128, 256, 128, 128, 128, 256};
+const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256, 16, 16, 32, 64, 256, 128};
+const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128, 128, 128, 128, 256, 128, 128, 128, 256, 128};
 
 int env_int(const char* name, int dflt) {
   const char* e = getenv(name);
@@ -606,8 +608,7 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   // configs 2 and 3): skinny M streams B with 16- to 64-row tiles, split over
   // K when too few column tiles cover the 256 CUs; larger M takes the largest
   // tile that still gives every CU a workgroup (256x256, then 256x128 from 144
-  // tiles -- 128 with block or MXFP4 scales -- then 128x128, split over K
-  // below 128).
+  // tiles -- 128 with block or MXFP4 scales -- then 128x128).
   auto tiles = [&](int bm, int bn) { return (long)cdiv(M, bm) * cdiv(N, bn); };
   int splits = 1;
   if (M <= 4) {
@@ -658,7 +659,9 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   } else if (tiles(256, 128) >= (smode >= 1 ? 128 : 144)) {
     p.kind = 9;
   } else {
-    p.kind = 2;
+    // 128x128 on 8 waves (64x32 wave tiles) -- 64x128 for MXFP4 when it gives
+    // 192 tiles -- split over K up to 128 128x128 tiles.
+    p.kind = (smode == 2 && tiles(64, 128) >= 192) ? 13 : 15;
     splits = tiles(128, 128) > 128 ? 1 : 2;
   }
   p.kind = env_int("TI_ROCM_FP8_KIND", p.kind);
@@ -687,6 +690,7 @@ void launch_grouped_smode(int kind, const GemmArgs& x, int max_mtiles, hipStream
     case 11: launch_grouped_cfg<16, 128, 128, 1, 8, 16, 6, SMODE>(x, max_mtiles, stream); break;
     case 12: launch_grouped_cfg<32, 128, 128, 1, 8, 16, 6, SMODE>(x, max_mtiles, stream); break;
     case 13: launch_grouped_cfg<64, 128, 128, 2, 4, 16, 4, SMODE>(x, max_mtiles, stream); break;
+    case 15: launch_grouped_cfg<128, 128, 128, 2, 4, 32, 3, SMODE>(x, max_mtiles, stream); break;
     default: launch_grouped_cfg<16, 128, 128, 1, 4, 16, 6, SMODE>(x, max_mtiles, stream); break;
   }
 }

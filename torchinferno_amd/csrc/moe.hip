@@ -116,17 +116,18 @@ struct Plan {
   int max_tiles;  // m-tile table capacity
 };
 
-Plan make_plan(int T, int k, int E) {
+Plan make_plan(int T, int k, int E, int smode) {
   const long R = (long)T * k;
   const long avg = (R + E - 1) / E;
   Plan p;
   // Measured at the config-4 shapes: 8-wave 16- / 32-row tiles for few rows
-  // per expert (T=64: avg 2; T=512: avg 16), 128x128 around avg 128.
-  p.kind = avg <= 8 ? 11 : (avg <= 48 ? 12 : (avg <= 160 ? 2 : 9));
+  // per expert (T=64: avg 2; T=512: avg 16); at avg 128 (T=4096) 256x128 for
+  // FP8 experts and 4-wave 128x128 for MXFP4 ones; 8-wave 128x128 between.
+  p.kind = avg <= 8 ? 11 : (avg <= 48 ? 12 : (avg <= 96 ? 15 : (smode == 2 ? 2 : 9)));
   const char* env = getenv("TI_ROCM_MOE_KIND");
   if (env && *env) {
     const int kk = atoi(env);
-    if (kk == 2 || kk == 5 || kk == 6 || kk == 9 || kk == 11 || kk == 12 || kk == 13) p.kind = kk;
+    if (kk == 2 || kk == 5 || kk == 6 || kk == 9 || kk == 11 || kk == 12 || kk == 13 || kk == 15) p.kind = kk;
   }
   p.bm = fp8::grouped_bm(p.kind);
   p.max_tiles = (int)(R / p.bm + E + 1);
@@ -322,8 +323,10 @@ static bool moe_shape_ok(int T, int k, int E, int H, int I) {
 
 extern "C" size_t ti_fp8_moe_workspace_bytes(int T, int k, int E, int H, int I) {
   if (!moe_shape_ok(T, k, E, H, I) || T == 0) return 0;
-  Plan p = make_plan(T, k, E);
-  return carve(nullptr, T, k, H, I, p).bytes;
+  // One size serves both weight formats (their plans may pick different tiles).
+  const size_t b1 = carve(nullptr, T, k, H, I, make_plan(T, k, E, 1)).bytes;
+  const size_t b2 = carve(nullptr, T, k, H, I, make_plan(T, k, E, 2)).bytes;
+  return b1 > b2 ? b1 : b2;
 }
 
 // Routed experts, shared by the block-FP8 (smode 1: e4m3 weights, 128x128
@@ -341,7 +344,7 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
                    ((uintptr_t)out & 3) == 0 && ((uintptr_t)s13 & 3) == 0 && ((uintptr_t)s2 & 3) == 0,
                "%s: hidden, w13, w2 must be 16-byte and out, scales 4-byte aligned", name);
   if (T == 0) return TI_OK;
-  Plan p = make_plan(T, k, E);
+  Plan p = make_plan(T, k, E, smode);
   Ws w = carve(nullptr, T, k, H, I, p);
   if (!workspace || workspace_bytes < w.bytes) {
     set_error("%s: workspace of %zu bytes required (got %zu)", name, w.bytes, workspace_bytes);
