@@ -218,3 +218,21 @@ def test_decode_kernel_eight_waves(dev, monkeypatch, plan, m, n):
     monkeypatch.setenv("TI_ROCM_W4A16_DECODE_PLAN", plan)
     out, ref = _run_gemm(dev, m, 2048, n, torch.float16 if m % 2 else torch.bfloat16, 60 + m)
     assert _rel_err(out.float().cpu().numpy(), ref) <= TOL
+
+
+# 16-wave tiles (four waves per SIMD): every instantiated (mr, nt, wk, ring),
+# with and without split-K, ragged M, both dtypes.
+@pytest.mark.parametrize("plan", ["64/2:2:2:1", "64/2:2:2:3", "32/2:4:2:1", "32/2:4:2:2", "32/1:4:3:1",
+                                  "32/1:4:3:3", "16/2:4:3:1", "16/2:4:3:2", "16/1:4:4:1", "16/1:4:4:3"])
+@pytest.mark.parametrize("m,n", [(40, 512), (100, 1024), (21, 256), (7, 512)])
+def test_decode_kernel_sixteen_waves(dev, monkeypatch, plan, m, n):
+    print(f"[int4] 16-wave plan {plan} M={m} N={n}", flush=True)
+    mr, plan = plan.split("/")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MIN_M", "1")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MAX_M", "4096")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_MR", mr)
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_WAVES", "16")
+    monkeypatch.setenv("TI_ROCM_W4A16_DECODE_PLAN", plan)
+    out, ref = _run_gemm(dev, m, 2048, n, torch.float16 if m % 2 else torch.bfloat16, 80 + m)
+    assert _rel_err(out.float().cpu().numpy(), ref) <= TOL
+
