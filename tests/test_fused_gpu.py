@@ -75,6 +75,26 @@ def test_swiglu_bit_exact_on_split_views(dev, dt, rows, n):
     assert np.array_equal(_codes(q), oq) and np.array_equal(s.cpu().numpy(), os_)
 
 
+def test_swiglu_every_bf16_gate_value(dev):
+    """Every finite bf16 gate value (all 2^16 bit patterns in order, 1,024 to a
+    row -- rows of like exponents -- with inf / NaN patterns replaced by 0),
+    up = 1 and up = -3: the bf16 path reads g / (1 + exp(-g)) from a per-workgroup table
+    covering 2^-25 <= |g| < 128 and closed forms outside, and must equal the
+    fp64 expression everywhere.  More rows than workgroups, so the
+    row-striding loop runs too."""
+    from torchinferno_amd.kernels import fused
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    bits[((bits >> 7) & 0xFF) == 0xFF] = 0                # inf / NaN -> +0
+    gate_np = (bits << 16).view(np.float32)
+    gate = torch.from_numpy(gate_np.copy()).to(torch.bfloat16).reshape(64, 1024)
+    gate = gate.repeat(9, 1).to(dev)                     # 576 rows > 512 workgroups
+    for u in (1.0, -3.0):
+        up = torch.full_like(gate, u)
+        q, s = fused.swiglu_fp8_per_token(gate, up)
+        oq, os_ = ofu.swiglu_fp8_per_token(_np(gate), _np(up), "bf16")
+        assert np.array_equal(_codes(q), oq) and np.array_equal(s.cpu().numpy(), os_)
+
+
 def test_zero_rows_and_errors(dev):
     from torchinferno_amd.kernels import fused
     x = torch.zeros((2, 64), device=dev, dtype=torch.bfloat16)

@@ -71,3 +71,30 @@ def test_exp_rounding_is_implementation_independent():
             nxt = np.where(e >= f64, np.nextafter(f, F32(np.inf)), np.nextafter(f, F32(0))).astype(np.float64)
             mid = (f64 + nxt) / 2
             assert (np.abs(e - mid) / e).min() >= 2.0 ** -51
+
+
+def test_exp_neg_closed_forms_outside_table_range():
+    """The bf16 SwiGLU kernel tabulates g / (1 + exp(-g)) only for exponent fields
+    102..133 (2^-25 <= |g| < 128).  Outside that range the fp64 expression,
+    rounded to fp32, is exactly 1 (|g| < 2^-25), 0 (g >= 128) or inf
+    (g <= -128) for every finite bf16 value."""
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    bits = bits[((bits >> 7) & 0xFF) != 0xFF]
+    g = (bits << 16).view(np.float32)
+    with np.errstate(over="ignore"):
+        e = np.exp(-g.astype(np.float64)).astype(np.float32)
+    field = (bits >> 7) & 0xFF
+    neg = ((bits >> 15) & 1) == 1
+    assert np.all(e[field < 102] == 1.0)
+    assert np.all(e[(field >= 134) & ~neg] == 0.0)
+    assert np.all(np.isposinf(e[(field >= 134) & neg]))
+    # and inside it the values are neither all 1 nor saturated (the table is needed)
+    inside = (field >= 102) & (field < 134)
+    assert np.any(e[inside] != 1.0) and np.all(np.isfinite(e[inside & ~neg]))
+    # so the quotient g / (1 + e) is g * 0.5, g and -0 there, bit for bit
+    with np.errstate(over="ignore", invalid="ignore"):
+        silu = (g / (np.float32(1.0) + e)).astype(np.float32)
+    lo, hi_pos, hi_neg = field < 102, (field >= 134) & ~neg, (field >= 134) & neg
+    assert np.array_equal(silu[lo].view(np.uint32), (g[lo] * np.float32(0.5)).view(np.uint32))
+    assert np.array_equal(silu[hi_pos].view(np.uint32), g[hi_pos].view(np.uint32))
+    assert np.all(silu[hi_neg].view(np.uint32) == np.uint32(0x80000000))

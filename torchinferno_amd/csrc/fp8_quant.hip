@@ -242,34 +242,75 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_quant_kernel(
   row_quant_store<V>(h, amax, n, q + row * n, s + row);
 }
 
+// silu(g) = g / (1 + exp(-g)) for bf16 g, exactly as the per-element
+// expression computes it (exp in fp64 rounded to fp32, then an IEEE fp32
+// quotient).  A bf16 value has 2^16 bit patterns; only those with
+// 2^-25 <= |g| < 128 (exponent field 102..133, 8192 patterns) need the full
+// expression: kSiluBf16 holds them, generated at build time by the same
+// expression in numpy (build_lib.py:write_silu_table; fp64 exp lies far enough
+// from every fp32 rounding boundary there that host and device round alike,
+// and a GPU test checks all 2^16 inputs).  Each workgroup copies the table to
+// LDS.  Elsewhere exp(-g) rounds to exactly 1 (|g| < 2^-25), 0 (g >= 128) or
+// inf (g <= -128), so silu(g) is g * 0.5, g or -0; inf and NaN take the full
+// expression.
+constexpr int kExpE0 = 102;       // first tabulated exponent field
+constexpr int kExpTab = 2 * 32 * 128;
+
+__device__ __align__(16) const uint32_t kSiluBf16[kExpTab] = {
+#include "silu_bf16_table.h"
+};
+
+__device__ __forceinline__ float silu_f64exp(float g) { return g / (1.0f + (float)exp(-(double)g)); }
+
+__device__ __forceinline__ float silu_bf16(float g, const float* tab) {
+  const uint32_t b = __float_as_uint(g) >> 16;
+  const uint32_t e = (b >> 7) & 0xFFu;
+  if (e - kExpE0 < 32u) return tab[((b >> 15) << 12) | ((e - kExpE0) << 7) | (b & 127u)];
+  if (e < (uint32_t)kExpE0) return g * 0.5f;
+  if (e == 0xFFu) return silu_f64exp(g);
+  return (b >> 15) ? -0.0f : g;
+}
+
 // SwiGLU -> per-token e4m3: act = g / (1 + exp(-g)) * u (exp in fp64, rounded
-// to fp32), rounded to the activation dtype.  Rows of gate/up are strided.
+// to fp32; bf16 inputs read the quotient from the table above), rounded to the
+// activation dtype.  Rows of gate/up are strided; workgroups stride over rows.
 template <int DT, int V>
 __global__ __launch_bounds__(kRowThreads) void swiglu_quant_kernel(const uint16_t* __restrict__ gate, long gstride,
                                                                    const uint16_t* __restrict__ up, long ustride,
-                                                                   int n, uint8_t* __restrict__ q,
+                                                                   int n, long rows, uint8_t* __restrict__ q,
                                                                    float* __restrict__ s) {
+  constexpr bool TAB = DT == TI_DTYPE_BF16;
   __shared__ float redf[kRowWaves];
-  const long row = blockIdx.x;
-  float a[V][8];
-  float amax = 0.f;
+  __shared__ __align__(16) float etab[TAB ? kExpTab : 1];
+  if constexpr (TAB) {
+    for (int i = threadIdx.x * 4; i < kExpTab; i += kRowThreads * 4)
+      *(uint4*)(etab + i) = *(const uint4*)(kSiluBf16 + i);
+    __syncthreads();
+  }
+  for (long row = blockIdx.x; row < rows; row += gridDim.x) {
+    float a[V][8];
+    float amax = 0.f;
 #pragma unroll
-  for (int j = 0; j < V; ++j) {
-    const int i = (j * kRowThreads + threadIdx.x) * 8;
-    if (i < n) {
-      float g[8], u[8];
-      load8<DT>(gate + row * gstride + i, g);
-      load8<DT>(up + row * ustride + i, u);
+    for (int j = 0; j < V; ++j) {
+      const int i = (j * kRowThreads + threadIdx.x) * 8;
+      if (i < n) {
+        float g[8], u[8];
+        load8<DT>(gate + row * gstride + i, g);
+        load8<DT>(up + row * ustride + i, u);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-const float ex = (float)exp(-(double)g[e]);
-        a[j][e] = round_act<DT>(g[e] / (1.0f + ex) * u[e]);
-        amax = fmaxf(amax, fabsf(a[j][e]));
+        for (int e = 0; e < 8; ++e) {
+          float sg;
+          if constexpr (TAB) sg = silu_bf16(g[e], etab);
+          else sg = silu_f64exp(g[e]);
+          a[j][e] = round_act<DT>(sg * u[e]);
+          amax = fmaxf(amax, fabsf(a[j][e]));
+        }
       }
     }
+    amax = row_max_f32(amax, redf);
+    row_quant_store<V>(a, amax, n, q + row * n, s + row);
+    __syncthreads();  // redf is rewritten by the next row
   }
-  amax = row_max_f32(amax, redf);
-  row_quant_store<V>(a, amax, n, q + row * n, s + row);
 }
 
 // Register-resident row width: the smallest V in {1, 2, 4, 8} with n <= 8192 V.
@@ -398,9 +439,11 @@ extern "C" int ti_fp8_swiglu_quant_per_token(const void* gate, long gate_row_str
                "ti_fp8_swiglu_quant_per_token: misaligned pointer");
   if (rows == 0) return TI_OK;
   const int v = row_vectors(n);
+  // bf16: at most two workgroups per CU, each building its exp table once.
+  const int grid = dtype == TI_DTYPE_BF16 ? (rows < 512 ? rows : 512) : rows;
   auto launch = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(rows), dim3(kRowThreads), 0, stream, (const uint16_t*)gate, gate_row_stride,
-                       (const uint16_t*)up, up_row_stride, n, xq, xs);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kRowThreads), 0, stream, (const uint16_t*)gate, gate_row_stride,
+                       (const uint16_t*)up, up_row_stride, n, (long)rows, xq, xs);
   };
   auto by_v = [&](auto dt) {
     constexpr int DT = decltype(dt)::value;
