@@ -222,8 +222,8 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const int* __restr
 }
 
 // h = bf16(w * silu(g) * u) over one sorted row's 128-wide block, then 1x128
-// e4m3 quant (act_quant).  One wave per (row, block); rows past the routed
-// count are skipped.
+// e4m3 quant (act_quant).  One wave per (row, four blocks); rows past the
+// routed count are skipped.
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __restrict__ gu, int I,
                                                            const float* __restrict__ route_w,
                                                            const int* __restrict__ route_of_pos,
@@ -232,40 +232,53 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
                                                            const int* __restrict__ tile_rows, long R,
                                                            float clamp_limit, uint8_t* __restrict__ hq,
                                                            float* __restrict__ hs) {
+  // One wave per (row, four 128-wide blocks); each 16-lane group owns a block,
+  // 8 elements (16-byte loads) per lane.
   const int lane = threadIdx.x & 63;
   const int IB = I / 128;
+  const int QB = (IB + 3) / 4;
   const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= R * IB) return;
-  const long p = item / IB;
-  const int blk = (int)(item % IB);
+  if (item >= R * QB) return;
+  const long p = item / QB;
+  const int blk = (int)(item % QB) * 4 + (lane >> 4);
   // Rows in use: tile table end (last tile's row0 + rows).
   const int nt = *num_rows_tiles;
   const long used = nt > 0 ? (long)tile_row0[nt - 1] + tile_rows[nt - 1] : 0;
   if (p >= used) return;
+  const bool on = blk < IB;
   const float w = route_w[route_of_pos[p]];
   const uint16_t* row = gu + p * 2 * I;
-  const int c = blk * 128 + lane * 2;
-  const uint32_t gw = *(const uint32_t*)(row + c);
-  const uint32_t uw = *(const uint32_t*)(row + I + c);
-  float h[2];
+  const int c = min(blk, IB - 1) * 128 + (lane & 15) * 8;
+  const uint4 gw = *(const uint4*)(row + c);
+  const uint4 uw = *(const uint4*)(row + I + c);
+  const uint32_t gv[4] = {gw.x, gw.y, gw.z, gw.w}, uv[4] = {uw.x, uw.y, uw.z, uw.w};
+  float h[8];
+  float amax = 0.f;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    float g = bf16_bits_to_f32((uint16_t)(gw >> (16 * i)));
-    float u = bf16_bits_to_f32((uint16_t)(uw >> (16 * i)));
+  for (int i = 0; i < 8; ++i) {
+    float g = bf16_bits_to_f32((uint16_t)(gv[i >> 1] >> (16 * (i & 1))));
+    float u = bf16_bits_to_f32((uint16_t)(uv[i >> 1] >> (16 * (i & 1))));
     if (clamp_limit > 0.f) {
       u = fminf(fmaxf(u, -clamp_limit), clamp_limit);
       g = fminf(g, clamp_limit);
     }
     const float act = g / (1.0f + expf(-g)) * u;
     h[i] = bf16_bits_to_f32(f32_to_bf16_bits(w * act));
+    amax = fmaxf(amax, fabsf(h[i]));
   }
-  float amax = wave_max(fmaxf(fabsf(h[0]), fabsf(h[1])));
+  // block max over the 16 lanes of the group
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
   amax = fmaxf(amax, 1e-4f);
   const float s = amax * (1.0f / kE4M3Max);
-  const uint32_t q0 = e4m3_encode(fminf(fmaxf(h[0] / s, -kE4M3Max), kE4M3Max));
-  const uint32_t q1 = e4m3_encode(fminf(fmaxf(h[1] / s, -kE4M3Max), kE4M3Max));
-  *(uint16_t*)(hq + p * I + c) = (uint16_t)(q0 | (q1 << 8));
-  if (lane == 0) hs[p * IB + blk] = s;
+  uint32_t q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = e4m3_encode(fminf(fmaxf(h[i] / s, -kE4M3Max), kE4M3Max));
+  if (on) {
+    *(uint2*)(hq + p * I + c) = make_uint2(q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24),
+                                           q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24));
+    if ((lane & 15) == 0) hs[p * IB + blk] = s;
+  }
 }
 
 // y[t] = bf16(sum over t's routes, in expert order, of fp32(out2[row])).
@@ -286,14 +299,25 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     eid[j] = e;
     pos[j] = p;
   }
-  for (int c = threadIdx.x * 2; c < H; c += 256 * 2) {
-    float a0 = 0.f, a1 = 0.f;
+  for (int c = threadIdx.x * 8; c < H; c += 256 * 8) {
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int j = 0; j < n; ++j) {
-      const uint32_t v = *(const uint32_t*)(out2 + (long)pos[j] * H + c);
-      a0 += bf16_bits_to_f32((uint16_t)(v & 0xFFFFu));
-      a1 += bf16_bits_to_f32((uint16_t)(v >> 16));
+      const uint4 v = *(const uint4*)(out2 + (long)pos[j] * H + c);
+      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] += bf16_bits_to_f32((uint16_t)(vv[i >> 1] >> (16 * (i & 1))));
     }
-    *(uint32_t*)(y + t * H + c) = (uint32_t)f32_to_bf16_bits(a0) | ((uint32_t)f32_to_bf16_bits(a1) << 16);
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = (uint32_t)f32_to_bf16_bits(a[2 * i]) | ((uint32_t)f32_to_bf16_bits(a[2 * i + 1]) << 16);
+    uint16_t* yc = y + t * H + c;
+    if (((uintptr_t)y & 15) == 0) {
+      *(uint4*)yc = make_uint4(o[0], o[1], o[2], o[3]);
+    } else {  // `out` need only be 4-byte aligned
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ((uint32_t*)yc)[i] = o[i];
+    }
   }
 }
 
@@ -378,7 +402,7 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
   fp8::launch_gemm_grouped(p.kind, smode, g, p.max_tiles, stream);
   TI_CHECK_LAUNCH("moe(w13)");
   // 4. swiglu x route weight -> 1x128 quant
-  const long items = R * (I / 128);
+  const long items = R * ((I / 128 + 3) / 4);
   hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, w.out1, I,
                      topk_weights, w.route_of_pos, w.num_tiles, w.tile_row0, w.tile_rows, R, clamp_limit, w.hq,
                      w.hs);
