@@ -565,6 +565,7 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
       case 12: launch_cfg<32, 128, 128, 1, 8, 16, 6, SMODE, ODT>(p, x, stream); break;
       case 13: launch_cfg<64, 128, 128, 2, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
       case 15: launch_cfg<128, 128, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
+      case 16: launch_cfg<256, 256, 128, 2, 4, 16, 2, SMODE, ODT>(p, x, stream); break;
       default: launch_cfg<256, 256, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
     }
   } else {
@@ -583,6 +584,7 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
       case 12: launch_cfg<32, 128, 128, 1, 8, 16, 6, SMODE, ODT>(p, x, stream); break;
       case 13: launch_cfg<64, 128, 128, 2, 4, 16, 4, SMODE, ODT>(p, x, stream); break;
       case 15: launch_cfg<128, 128, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
+      case 16: launch_cfg<256, 256, 128, 2, 4, 16, 2, SMODE, ODT>(p, x, stream); break;
       case 14:
         if constexpr (SMODE == 0) launch_cfg<256, 256, 128, 4, 4, 32, 2, SMODE, ODT>(p, x, stream);
         break;
@@ -591,8 +593,8 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
   }
 }
 
-const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256, 16, 16, 32, 64, 256, 128};
-const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128, 128, 128, 128, 256, 128, 128, 128, 256, 128};
+const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256, 16, 16, 32, 64, 256, 128, 256};
+const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128, 128, 128, 128, 256, 128, 128, 128, 256, 128, 256};
 
 int env_int(const char* name, int dflt) {
   const char* e = getenv(name);
@@ -653,9 +655,11 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
     }
   } else if (tiles(256, 256) >= 256) {
     // Per-token FP8 runs the 256x256 tile on 16 waves (4 per SIMD, 64x64 wave
-    // tiles: 4-10% faster); the block / MXFP4 folds need more registers than
-    // 16 waves leave, so they keep 8.
-    p.kind = smode == 0 ? 14 : 1;
+    // tiles: 4-10% faster).  The block / MXFP4 folds need more registers than
+    // 16 waves leave; they keep 8 waves with 16x16x128 MFMAs, whose 4-register
+    // partial sums leave room to fold one tile while the next one's MFMAs run
+    // (2-4% over the 32x32x64 form).
+    p.kind = smode == 0 ? 14 : 16;
   } else if (tiles(256, 128) >= (smode >= 1 ? 128 : 144)) {
     p.kind = 9;
   } else {
