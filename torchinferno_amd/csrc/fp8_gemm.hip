@@ -381,15 +381,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
         float srow[MM::NACC];
 #pragma unroll
         for (int e = 0; e < MM::NACC; ++e) srow[e] = sS[wm * TM + fm * MF + MM::row(e, lane)];
+        // All FN partial sums first, then their folds: each fold then
+        // waits only on its own MFMA chain, the later chains still running.
+        acc_t pf[FN];
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
-          acc_t p;
 #pragma unroll
-          for (int e = 0; e < MM::NACC; ++e) p[e] = 0.f;
+          for (int e = 0; e < MM::NACC; ++e) pf[fn][e] = 0.f;
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) p = MM::mma4(af[ks], bf[ks][fn], p, eb[ks][fn]);
-          fold(fm, fn, p, srow);
+          for (int ks = 0; ks < KS; ++ks) pf[fn] = MM::mma4(af[ks], bf[ks][fn], pf[fn], eb[ks][fn]);
         }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) fold(fm, fn, pf[fn], srow);
         if constexpr (DEFER) {
 #pragma unroll
           for (int e = 0; e < MM::NACC; ++e) sd[fm][e] = srow[e];
@@ -426,15 +429,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
         float srow[MM::NACC];
 #pragma unroll
         for (int e = 0; e < MM::NACC; ++e) srow[e] = sS[wm * TM + fm * MF + MM::row(e, lane)] * sbv;
+        // All FN partial sums first, then their folds: each fold then
+        // waits only on its own MFMA chain, the later chains still running.
+        acc_t pf[FN];
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
-          acc_t p;
 #pragma unroll
-          for (int e = 0; e < MM::NACC; ++e) p[e] = 0.f;
+          for (int e = 0; e < MM::NACC; ++e) pf[fn][e] = 0.f;
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) p = MM::mma(af[ks], bf[ks][fn], p);
-          fold(fm, fn, p, srow);
+          for (int ks = 0; ks < KS; ++ks) pf[fn] = MM::mma(af[ks], bf[ks][fn], pf[fn]);
         }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) fold(fm, fn, pf[fn], srow);
         if constexpr (DEFER) {
 #pragma unroll
           for (int e = 0; e < MM::NACC; ++e) sd[fm][e] = srow[e];
