@@ -527,6 +527,15 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 //   7  BM=128 BN=128, 4 waves 2x2 (wave 64x64),   32x32 MFMA            64      6   -- mid M
 //   8  BM=256 BN=128, 4 waves 2x2 (wave 128x64),  32x32 MFMA            64      6   -- prefill
 //   9  BM=256 BN=128, 8 waves 4x2 (wave 64x64),   32x32 MFMA            128     3   -- prefill
+//  10  BM=16  BN=256, 8 waves 1x8 (wave 16x32),   16x16 MFMA            128     4   -- decode (tuning)
+//  11  BM=16  BN=128, 8 waves 1x8 (wave 16x16),   16x16 MFMA            128     6   -- decode
+//  12  BM=32  BN=128, 8 waves 1x8 (wave 32x16),   16x16 MFMA            128     6   -- small M
+//  13  BM=64  BN=128, 8 waves 2x4 (wave 32x32),   16x16 MFMA            128     4   -- small M
+//  14  BM=256 BN=256, 16 waves 4x4 (wave 64x64),  32x32 MFMA            128     2   -- prefill (per-token)
+//  15  BM=128 BN=128, 8 waves 2x4 (wave 64x32),   32x32 MFMA            128     3   -- mid M
+//  16  BM=256 BN=256, 8 waves 2x4 (wave 128x64),  16x16 MFMA            128     2   -- prefill (scaled)
+// The 8- and 16-wave kinds put two or four waves on each SIMD, which hides the
+// per-step barrier -> LDS read -> MFMA -> fold latency of one wave.
 template <int BM, int BN, int BK, int R, int SMODE>
 constexpr int cfg_lds() {
   const int sa = SMODE >= 1 ? ((BM * 4 + 255) / 256) * 256 : 0;
