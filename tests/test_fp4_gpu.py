@@ -46,7 +46,7 @@ def test_fp4_gemm_matches_oracle(dev, m, n, k):
     assert _rel_err(y.float().cpu().numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("kind", ["1", "2", "3", "5", "6", "9", "10", "11", "12", "13", "15", "16"])
+@pytest.mark.parametrize("kind", ["1", "2", "3", "5", "6", "9", "10", "11", "12", "13", "15", "16", "17"])
 @pytest.mark.parametrize("splits", ["1", "3"])
 def test_fp4_gemm_every_kind(dev, monkeypatch, kind, splits):
     """Both scale layouts: the checkpoint's [N, K/32] and the step-major copy."""
@@ -140,7 +140,7 @@ def _mxfp4_experts(e, h, inter, seed, dev):
 
 
 @pytest.mark.parametrize("t,k", [(1, 1), (9, 2), (64, 4), (300, 8)])
-@pytest.mark.parametrize("kind", ["auto", "2", "5", "6", "9", "11", "12", "13", "15"])
+@pytest.mark.parametrize("kind", ["auto", "2", "5", "6", "9", "11", "12", "13", "15", "17"])
 def test_mxfp4_moe_matches_oracle(dev, monkeypatch, t, k, kind):
     from torchinferno_amd.kernels import moe as tmoe
     print(f"[fp4] moe T={t} k={k} kind={kind}", flush=True)

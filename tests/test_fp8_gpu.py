@@ -222,7 +222,7 @@ def test_rowcol_ragged(dev, m, n):
     assert err <= TOL, err
 
 
-@pytest.mark.parametrize("kind", range(17))
+@pytest.mark.parametrize("kind", range(18))
 @pytest.mark.parametrize("mode", ["rowcol", "block"])
 def test_every_tile_kind(dev, monkeypatch, kind, mode):
     """Each tile configuration, forced, on a ragged problem, with and without split-K."""

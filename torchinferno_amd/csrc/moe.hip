@@ -121,13 +121,15 @@ Plan make_plan(int T, int k, int E, int smode) {
   const long avg = (R + E - 1) / E;
   Plan p;
   // Measured at the config-4 shapes: 8-wave 16- / 32-row tiles for few rows
-  // per expert (T=64: avg 2; T=512: avg 16); at avg 128 (T=4096) 256x128 for
-  // FP8 experts and 4-wave 128x128 for MXFP4 ones; 8-wave 128x128 between.
-  p.kind = avg <= 8 ? 11 : (avg <= 48 ? 12 : (avg <= 96 ? 15 : (smode == 2 ? 2 : 9)));
+  // per expert (T=64: avg 2; T=512: avg 16), 8-wave 128x256 at avg 128
+  // (T=4096: one m-tile per expert and half the activation re-reads of
+  // 128x128; -20% FP8, -4% MXFP4), 8-wave 128x128 between.
+  (void)smode;
+  p.kind = avg <= 8 ? 11 : (avg <= 48 ? 12 : (avg <= 96 ? 15 : 17));
   const char* env = getenv("TI_ROCM_MOE_KIND");
   if (env && *env) {
     const int kk = atoi(env);
-    if (kk == 2 || kk == 5 || kk == 6 || kk == 9 || kk == 11 || kk == 12 || kk == 13 || kk == 15) p.kind = kk;
+    if (kk == 2 || kk == 5 || kk == 6 || kk == 9 || kk == 11 || kk == 12 || kk == 13 || kk == 15 || kk == 17) p.kind = kk;
   }
   p.bm = fp8::grouped_bm(p.kind);
   p.max_tiles = (int)(R / p.bm + E + 1);
