@@ -632,9 +632,12 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   auto tiles = [&](int bm, int bn) { return (long)cdiv(M, bm) * cdiv(N, bn); };
   int splits = 1;
   if (M <= 4) {
+    // Split over K below 128 column tiles: up to 4 ways, 8 at deep K (down
+    // M=1, K=28672: 51.7 -> 44.1 us).
     p.kind = 3;
     const long t = tiles(16, 256);
-    splits = t >= 128 ? 1 : (int)(cdiv(256, (int)t) < 4 ? cdiv(256, (int)t) : 4);
+    const int cap = K >= 16384 ? 8 : 4;
+    splits = t >= 128 ? 1 : (int)(cdiv(256, (int)t) < cap ? cdiv(256, (int)t) : cap);
   } else if (M <= 16) {
     // 8-wave 16x128 tiles: two waves per SIMD hide each other's per-step
     // LDS/MFMA latency (12-24% faster than the 4-wave tile at M=16).
