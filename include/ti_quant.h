@@ -116,6 +116,13 @@ int ti_w4a16_gemm(const void* a, int dtype, const int32_t* packed_weight,
 int ti_fp8_quant_per_token(const void* x, int x_dtype, int M, int K, float eps,
                            uint8_t* xq, float* xs, hipStream_t stream);
 
+/* Self-check of the e4m3 encoders (no reference counterpart: test support).
+ * Runs every fp32 bit pattern through the software round-to-nearest-even
+ * encoder and the gfx950 conversion instruction and adds to counts[0] the
+ * disagreements on finite |x| < 480, to counts[1] those elsewhere.  counts:
+ * two zeroed device uint64. */
+int ti_fp8_e4m3_selfcheck(unsigned long long* counts, hipStream_t stream);
+
 /* 1 x block_size activation quant (block_size == 128): per (row, block)
  * s = max(amax, 1e-4) * (1/448) -- or 2^ceil(log2(that)) if round_scale --
  * xq = e4m3(clamp(x / s, -448, 448)).  Replaces act_quant

@@ -31,6 +31,20 @@ __device__ __forceinline__ uint32_t e4m3_encode(float x) {
   return mag | sign;
 }
 
+// Two fp32 -> e4m3fn codes by the gfx950 conversion instruction (round to
+// nearest even): low byte x0, high byte x1.  Agrees with e4m3_encode for every
+// finite |x| < 480 (ti_fp8_e4m3_selfcheck compares all 2^32 inputs); callers
+// keep their inputs in that range.
+__device__ __forceinline__ uint32_t e4m3_encode2_hw(float x0, float x1) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x0, x1, 0, false) & 0xFFFFu;
+}
+
+// Eight values (each finite, |y| < 480) -> eight e4m3fn bytes, in order.
+__device__ __forceinline__ uint2 e4m3_pack8_hw(const float (&y)[8]) {
+  return make_uint2(e4m3_encode2_hw(y[0], y[1]) | (e4m3_encode2_hw(y[2], y[3]) << 16),
+                    e4m3_encode2_hw(y[4], y[5]) | (e4m3_encode2_hw(y[6], y[7]) << 16));
+}
+
 template <int DT>
 __device__ __forceinline__ float act_to_f32(uint16_t h) {
   if constexpr (DT == TI_DTYPE_F16) return f16_bits_to_f32(h);

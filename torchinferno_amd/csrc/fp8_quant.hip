@@ -70,10 +70,10 @@ __global__ __launch_bounds__(256) void quant_per_token_kernel(const uint16_t* __
   for (int i = threadIdx.x * 8; i < K; i += 256 * 8) {
     float f[8];
     load8<DT>(xr + i, f);
-    uint32_t c[8];
+    float y[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) c[e] = e4m3_encode(f[e] / sc);
-    *(uint2*)(qr + i) = pack8(c);
+    for (int e = 0; e < 8; ++e) y[e] = f[e] / sc;  // |y| <= 448 by the choice of sc
+    *(uint2*)(qr + i) = e4m3_pack8_hw(y);
   }
 }
 
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void quant_block_kernel(const uint16_t* __rest
   }
   const float y0 = fminf(fmaxf(f0 / sc, -kE4M3Max), kE4M3Max);
   const float y1 = fminf(fmaxf(f1 / sc, -kE4M3Max), kE4M3Max);
-  *(uint16_t*)(q + off) = (uint16_t)(e4m3_encode(y0) | (e4m3_encode(y1) << 8));
+  *(uint16_t*)(q + off) = (uint16_t)e4m3_encode2_hw(y0, y1);
   if (lane == 0) s[s_layout ? (long)kb * M + row : row * KB + kb] = sc;
 }
 
@@ -182,10 +182,10 @@ __device__ __forceinline__ void row_quant_store(float (&v)[V][8], float amax, in
   for (int j = 0; j < V; ++j) {
     const int i = (j * kRowThreads + threadIdx.x) * 8;
     if (i < n) {
-      uint32_t c[8];
+      float y[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) c[e] = e4m3_encode(v[j][e] / sc);
-      *(uint2*)(qr + i) = pack8(c);
+      for (int e = 0; e < 8; ++e) y[e] = v[j][e] / sc;  // |y| <= 448 by the choice of sc
+      *(uint2*)(qr + i) = e4m3_pack8_hw(y);
     }
   }
 }
@@ -313,6 +313,23 @@ __global__ __launch_bounds__(kRowThreads) void swiglu_quant_kernel(const uint16_
   }
 }
 
+// Every fp32 bit pattern through both encoders; counts[0] = disagreements on
+// finite |x| < 480, counts[1] = disagreements elsewhere (NaN, inf, overflow).
+__global__ __launch_bounds__(256) void e4m3_selfcheck_kernel(unsigned long long* __restrict__ counts) {
+  unsigned long long in_range = 0, outside = 0;
+  const uint64_t stride = (uint64_t)gridDim.x * 256;
+  for (uint64_t p = (uint64_t)blockIdx.x * 256 + threadIdx.x; p < (1ull << 31); p += stride) {
+    const float x0 = __uint_as_float((uint32_t)(2 * p)), x1 = __uint_as_float((uint32_t)(2 * p + 1));
+    const uint32_t hw = e4m3_encode2_hw(x0, x1);
+    const bool ok0 = (hw & 0xFFu) == e4m3_encode(x0), ok1 = (hw >> 8) == e4m3_encode(x1);
+    const bool dom0 = fabsf(x0) < 480.0f, dom1 = fabsf(x1) < 480.0f;  // false for NaN
+    in_range += (dom0 && !ok0) + (dom1 && !ok1);
+    outside += (!dom0 && !ok0) + (!dom1 && !ok1);
+  }
+  if (in_range) atomicAdd(&counts[0], in_range);
+  if (outside) atomicAdd(&counts[1], outside);
+}
+
 // Register-resident row width: the smallest V in {1, 2, 4, 8} with n <= 8192 V.
 inline int row_vectors(int n) { return n <= 8192 ? 1 : n <= 16384 ? 2 : n <= 32768 ? 4 : 8; }
 constexpr int kRowMaxN = 8 * kRowThreads * 8;
@@ -325,6 +342,13 @@ bool act_dtype_ok(int dt) { return dt == TI_DTYPE_F16 || dt == TI_DTYPE_BF16; }
 
 using namespace ti;
 using namespace ti::fp8;
+
+extern "C" int ti_fp8_e4m3_selfcheck(unsigned long long* counts, hipStream_t stream) {
+  TI_CHECK_ARG(counts, "ti_fp8_e4m3_selfcheck: null pointer");
+  hipLaunchKernelGGL(e4m3_selfcheck_kernel, dim3(8192), dim3(256), 0, stream, counts);
+  TI_CHECK_LAUNCH("ti_fp8_e4m3_selfcheck");
+  return TI_OK;
+}
 
 extern "C" int ti_fp8_quant_per_token(const void* x, int x_dtype, int M, int K, float eps,
                                       uint8_t* xq, float* xs, hipStream_t stream) {

@@ -273,12 +273,11 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
   for (int o = 1; o < 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
   amax = fmaxf(amax, 1e-4f);
   const float s = amax * (1.0f / kE4M3Max);
-  uint32_t q[8];
+  float y[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = e4m3_encode(fminf(fmaxf(h[i] / s, -kE4M3Max), kE4M3Max));
+  for (int i = 0; i < 8; ++i) y[i] = fminf(fmaxf(h[i] / s, -kE4M3Max), kE4M3Max);
   if (on) {
-    *(uint2*)(hq + p * I + c) = make_uint2(q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24),
-                                           q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24));
+    *(uint2*)(hq + p * I + c) = fp8::e4m3_pack8_hw(y);
     if ((lane & 15) == 0) hs[p * IB + blk] = s;
   }
 }
