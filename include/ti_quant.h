@@ -123,6 +123,14 @@ int ti_fp8_quant_per_token(const void* x, int x_dtype, int M, int K, float eps,
  * two zeroed device uint64. */
 int ti_fp8_e4m3_selfcheck(unsigned long long* counts, hipStream_t stream);
 
+/* Self-check of the fp32 -> bf16 roundings (no reference counterpart: test
+ * support): every fp32 bit pattern through the integer round-to-nearest-even
+ * and the gfx950 conversion instruction the kernels use; adds to counts[0] the
+ * disagreements on
+ * non-NaN inputs, to counts[1] those on NaN inputs.  counts: two zeroed device
+ * uint64. */
+int ti_bf16_round_selfcheck(unsigned long long* counts, hipStream_t stream);
+
 /* 1 x block_size activation quant (block_size == 128): per (row, block)
  * s = max(amax, 1e-4) * (1/448) -- or 2^ceil(log2(that)) if round_scale --
  * xq = e4m3(clamp(x / s, -448, 448)).  Replaces act_quant

@@ -165,3 +165,16 @@ def test_e4m3_hardware_encoder_matches_software_everywhere_in_range(dev):
     in_range, outside = (int(v) for v in counts.cpu())
     print(f"[fp8] e4m3 encoders disagree on {in_range} in-range and {outside} other inputs", flush=True)
     assert in_range == 0
+
+
+def test_bf16_hardware_rounding_matches_software_on_every_number(dev):
+    """Every kernel rounds fp32 to bf16 with the gfx950 conversion instruction;
+    it equals the integer round-to-nearest-even (NaN -> quiet NaN) rounding on
+    all 2^32 fp32 bit patterns."""
+    from torchinferno_amd import _lib
+    counts = torch.zeros(2, dtype=torch.int64, device=dev)
+    _lib.call("ti_bf16_round_selfcheck", counts.data_ptr(), _lib.stream_of(counts))
+    torch.cuda.synchronize()
+    num, nan = (int(v) for v in counts.cpu())
+    print(f"[bf16] roundings disagree on {num} numbers and {nan} NaNs", flush=True)
+    assert num == 0 and nan == 0

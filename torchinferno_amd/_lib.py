@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ti_fp8_quant_per_token": (_i, [_vp, _i, _i, _i, _f, _vp, _vp, _vp]),
     "ti_fp8_quant_block": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp]),
     "ti_fp8_e4m3_selfcheck": (_i, [_vp, _vp]),
+    "ti_bf16_round_selfcheck": (_i, [_vp, _vp]),
     "ti_fp8_quant_tensor": (_i, [_vp, _i, ctypes.c_long, _vp, _vp, _vp]),
     "ti_fp8_rmsnorm_quant_per_token": (_i, [_vp, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _vp]),
     "ti_fp8_swiglu_quant_per_token": (_i, [_vp, ctypes.c_long, _vp, ctypes.c_long, _i, _i, _i, _vp, _vp, _vp]),

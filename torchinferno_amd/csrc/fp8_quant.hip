@@ -330,6 +330,21 @@ __global__ __launch_bounds__(256) void e4m3_selfcheck_kernel(unsigned long long*
   if (outside) atomicAdd(&counts[1], outside);
 }
 
+// Every fp32 bit pattern through both bf16 roundings; counts[0] =
+// disagreements on non-NaN inputs, counts[1] = on NaN inputs.
+__global__ __launch_bounds__(256) void bf16_selfcheck_kernel(unsigned long long* __restrict__ counts) {
+  unsigned long long num = 0, nan = 0;
+  const uint64_t stride = (uint64_t)gridDim.x * 256;
+  for (uint64_t p = (uint64_t)blockIdx.x * 256 + threadIdx.x; p < (1ull << 32); p += stride) {
+    const float x = __uint_as_float((uint32_t)p);
+    const bool bad = f32_to_bf16_bits(x) != f32_to_bf16_bits_sw(x);
+    if (x == x) num += bad;
+    else nan += bad;
+  }
+  if (num) atomicAdd(&counts[0], num);
+  if (nan) atomicAdd(&counts[1], nan);
+}
+
 // Register-resident row width: the smallest V in {1, 2, 4, 8} with n <= 8192 V.
 inline int row_vectors(int n) { return n <= 8192 ? 1 : n <= 16384 ? 2 : n <= 32768 ? 4 : 8; }
 constexpr int kRowMaxN = 8 * kRowThreads * 8;
@@ -347,6 +362,13 @@ extern "C" int ti_fp8_e4m3_selfcheck(unsigned long long* counts, hipStream_t str
   TI_CHECK_ARG(counts, "ti_fp8_e4m3_selfcheck: null pointer");
   hipLaunchKernelGGL(e4m3_selfcheck_kernel, dim3(8192), dim3(256), 0, stream, counts);
   TI_CHECK_LAUNCH("ti_fp8_e4m3_selfcheck");
+  return TI_OK;
+}
+
+extern "C" int ti_bf16_round_selfcheck(unsigned long long* counts, hipStream_t stream) {
+  TI_CHECK_ARG(counts, "ti_bf16_round_selfcheck: null pointer");
+  hipLaunchKernelGGL(bf16_selfcheck_kernel, dim3(8192), dim3(256), 0, stream, counts);
+  TI_CHECK_LAUNCH("ti_bf16_round_selfcheck");
   return TI_OK;
 }
 

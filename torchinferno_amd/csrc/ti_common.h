@@ -49,12 +49,17 @@ void set_error(const char* fmt, ...);
   } while (0)
 
 // fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+// fp32 -> bf16, round to nearest even; NaN -> quiet NaN.  The integer form;
+// the kernels use f32_to_bf16_bits, one gfx950 v_cvt_pk_bf16_f32, which gives
+// the same bits for all 2^32 inputs (ti_bf16_round_selfcheck compares them).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits_sw(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
   u += 0x7fffu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
 }
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
   return __uint_as_float(((uint32_t)h) << 16);
