@@ -64,7 +64,7 @@ def test_per_channel_weight_quant_bit_exact(dev):
 
 
 @pytest.mark.parametrize("round_scale", [False, True])
-@pytest.mark.parametrize("m,k", [(1, 128), (5, 7168), (64, 18432)])
+@pytest.mark.parametrize("m,k", [(1, 128), (3, 640), (5, 7168), (64, 18432)])
 def test_block_act_quant_bit_exact(dev, round_scale, m, k):
     from torchinferno_amd.kernels import block_fp8 as tb
     g = torch.Generator().manual_seed(k + m)
@@ -72,6 +72,22 @@ def test_block_act_quant_bit_exact(dev, round_scale, m, k):
     x[0, :128] = 0  # an all-zero block takes the 1e-4 floor
     y, s = tb.act_quant(x.to(dev), 128, "ue8m0" if round_scale else None)
     oq, os_ = ofp8.act_quant_block(x.float().numpy(), 128, round_scale)
+    assert np.array_equal(_codes(y), oq)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), os_.view(np.uint32))
+
+
+@pytest.mark.parametrize("shift", [2, 8])
+def test_block_act_quant_unaligned_input(dev, shift):
+    """An input that starts 4 bytes past a 16-byte boundary takes the 4-byte-access kernel,
+    16 bytes past one the 16-byte kernel; both give the oracle's codes and scales."""
+    from torchinferno_amd.kernels import block_fp8 as tb
+    m, k = 7, 896
+    g = torch.Generator().manual_seed(shift)
+    flat = (torch.randn(m * k + shift, generator=g) * 2).to(torch.bfloat16)
+    xd = flat.to(dev)[shift:].view(m, k)
+    assert (xd.data_ptr() % 16 != 0) == (shift == 2)
+    y, s = tb.act_quant(xd)
+    oq, os_ = ofp8.act_quant_block(flat[shift:].view(m, k).float().numpy())
     assert np.array_equal(_codes(y), oq)
     assert np.array_equal(s.cpu().numpy().view(np.uint32), os_.view(np.uint32))
 
