@@ -362,7 +362,7 @@ def _moe_sweep(L, dev, label, entry, w13, s13, w2, s2, e, h, inter, k, per_exper
             _check("route", L.ti_moe_route_topk(logits.data_ptr(), t, e, k, 1, 1.0, wts.data_ptr(), ids.data_ptr(), st))
             lay = (1,) if entry == "ti_fp4_moe" else ()
             _check("moe", fn(x.data_ptr(), wts.data_ptr(), ids.data_ptr(), t, k, w13.data_ptr(),
-                             s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), *lay, e, h, inter, 0.0,
+                             s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), *lay, e, h, inter, 0.0, 0,
                              out.data_ptr(), wsp, need, st))
 
         timed_burst([launch], 2, stream)

@@ -110,11 +110,18 @@ int ti_w4a16_gemm(const void* a, int dtype, const int32_t* packed_weight,
 /* Per-row dynamic quant: xs[m] = max(amax_k |x[m,k]| / 448, eps),
  * xq[m,k] = e4m3(x[m,k] / xs[m]).  Replaces the per-token activation quant
  * (Triton _row_scale_cast_fp8 / sgl_per_token_quant_fp8,
- * src/torchinferno/kernels/fp8.py:53-72,99-116,234-238; eps 1e-10) and, run
- * over a weight's rows, quantize_weight_fp8_per_channel (fp8.py:129-138).
- * x fp16/bf16 [M,K] 16-byte aligned, K % 8 == 0; xq [M,K]; xs [M]. */
+ * src/torchinferno/kernels/fp8.py:53-72,99-116,234-238; eps 1e-10).
+ * x fp16/bf16 [M,K] 16-byte aligned, K % 8 == 0; xq [M,K] 8-byte aligned; xs [M]. */
 int ti_fp8_quant_per_token(const void* x, int x_dtype, int M, int K, float eps,
                            uint8_t* xq, float* xs, hipStream_t stream);
+
+/* Per-output-channel weight quant: ws[n] = max(amax_k |w[n,k]| * fl32(1/448), 1e-10),
+ * wq[n,k] = e4m3(w[n,k] / ws[n]).  Replaces quantize_weight_fp8_per_channel
+ * (src/torchinferno/kernels/fp8.py:129-138), whose ``amax.float() / 448.0`` torch
+ * evaluates on the GPU as a multiply by the fp32 reciprocal.  w fp16/bf16 [N,K]
+ * 16-byte aligned, K % 8 == 0; wq [N,K] 8-byte aligned; ws [N]. */
+int ti_fp8_quant_weight_per_channel(const void* w, int w_dtype, int N, int K, uint8_t* wq,
+                                    float* ws, hipStream_t stream);
 
 /* Self-check of the e4m3 encoders (no reference counterpart: test support).
  * Runs every fp32 bit pattern through the software round-to-nearest-even
@@ -253,11 +260,14 @@ size_t ti_fp8_moe_workspace_bytes(int T, int k, int E, int H, int I);
  *   outside [0,E) are skipped); w13 e4m3 [E, 2I, H] = [w1; w3] per expert,
  *   s13 fp32 [E, 2I/128, H/128]; w2 e4m3 [E, H, I], s2 fp32 [E, H/128, I/128];
  *   clamp_limit > 0 clamps gate <= limit and |up| <= limit (swiglu_limit);
+ *   round_scale != 0 gives both activation quants power-of-two scales
+ *   (act_quant with scale_fmt "ue8m0", the DSv4 checkpoint setting,
+ *   tensor_parallel.py:195-207,1199-1211);
  *   out bf16 [T,H].  H, I multiples of 128.  Deterministic. */
 int ti_fp8_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids,
                int T, int k, const uint8_t* w13, const float* s13, const uint8_t* w2,
-               const float* s2, int E, int H, int I, float clamp_limit, void* out,
-               void* workspace, size_t workspace_bytes, hipStream_t stream);
+               const float* s2, int E, int H, int I, float clamp_limit, int round_scale,
+               void* out, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* The same routed experts with MXFP4 weights (DSv4 expert_dtype "fp4"): every
  * w*_e is an e2m1 Linear with E8M0 scales per 32 K, applied as ti_fp4_gemm
@@ -270,7 +280,8 @@ int ti_fp8_moe(const void* hidden, const float* topk_weights, const int32_t* top
 int ti_fp4_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids,
                int T, int k, const uint8_t* w13, const uint8_t* s13, const uint8_t* w2,
                const uint8_t* s2, int scale_layout, int E, int H, int I, float clamp_limit,
-               void* out, void* workspace, size_t workspace_bytes, hipStream_t stream);
+               int round_scale, void* out, void* workspace, size_t workspace_bytes,
+               hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -3,12 +3,27 @@
 Reference arithmetic followed (all fp32, IEEE division, RNE cast to e4m3):
 
 * Per-output-channel weight quant -- src/torchinferno/kernels/fp8.py:129-138:
-  ``s[n] = max(amax_k |W[n,k]| / 448, 1e-10)``, ``Wq = W / s`` -> e4m3.
-* Tensorwise weight quant -- fp8.py:119-126: ``s = max(amax / 448, 1e-6)``.
+  ``s[n] = max(amax_k |W[n,k]| / 448, 1e-10)``, ``Wq = W / s`` -> e4m3.  The
+  reference evaluates ``amax.to(float32) / 448.0`` with torch on the weight's
+  GPU, where ATen turns division by a host Python scalar into a multiply by the
+  fp32 reciprocal: ``s = amax * fl32(1/448)`` (that differs from the quotient in
+  about half of all amax values, by one ulp).  ``W.float() / s`` divides by a
+  device tensor, so that one is an IEEE quotient.
+* Tensorwise weight quant -- fp8.py:119-126:
+  ``(W.abs().amax() / 448).clamp(min=1e-6).to(float32)``: the amax, the
+  product by fl32(1/448) and the clamp all stay in the weight's dtype, so the
+  product is rounded to bf16/fp16 before the clamp (whose bound is
+  ``dtype(1e-6)``) and the cast to fp32.
 * Per-token activation quant -- the Triton ``_row_scale_cast_fp8`` at
   fp8.py:53-72: ``s[m] = max(amax_k |x[m,k]| / 448, 1e-10)``, ``xq = x / s``.
-* Tensorwise activation quant -- fp8.py:141-181: ``s = max(amax/448, 1e-6)``
-  (or a caller scale), ``xq = x * (1/s)`` (multiply by the reciprocal, fp8.py:49-51).
+* Tensorwise activation quant -- fp8.py:141-181: the same dtype-rounded
+  ``max(amax/448, 1e-6)`` as the tensorwise weight scale (fp8.py:154-155), or a
+  caller scale; ``inv = 1/s`` (``scale.reciprocal()``, an IEEE fp32 quotient),
+  ``xq = x * inv`` (fp8.py:49-51).
+* The per-token activation scale comes from a Triton or sgl-kernel provider
+  (fp8.py:53-72,234-238) that divides ``amax / 448.0``; its rounding is the
+  provider's and is not pinned by anything in the reference, so the oracle uses
+  the IEEE quotient.
 * W8A8 linear -- fp8.py:250-327 (``_scaled_mm`` with ``scale_a [M,1]``,
   ``scale_b [1,N]``): ``out[m,n] = (sum_k xq[m,k] wq[n,k]) * xs[m] * ws[n]``.
 * DeepSeek 1x128 activation quant -- src/torchinferno/kernels/
@@ -33,22 +48,34 @@ from __future__ import annotations
 
 import numpy as np
 
-from .numerics import E4M3_MAX, e4m3_decode, e4m3_encode
+from .numerics import E4M3_MAX, e4m3_decode, e4m3_encode, round_to
 
 F32 = np.float32
 _INV_MAX = F32(1.0) / F32(E4M3_MAX)  # 1/448 rounded to fp32, the TileLang constant
 
 
 def quantize_weight_fp8_per_channel(w_nk: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-    """[N,K] fp32 (bf16 values) -> (codes uint8 [N,K], scale fp32 [1,N])."""
+    """[N,K] fp32 (bf16 values) -> (codes uint8 [N,K], scale fp32 [1,N]).
+    ``s = max(amax * fl32(1/448), 1e-10)`` -- ATen's GPU division by a host scalar."""
     w = np.asarray(w_nk, dtype=F32)
-    s = np.maximum(np.abs(w).max(axis=1, keepdims=True) / F32(E4M3_MAX), F32(1e-10)).astype(F32)
+    s = np.maximum((np.abs(w).max(axis=1, keepdims=True) * _INV_MAX).astype(F32), F32(1e-10)).astype(F32)
     return e4m3_encode(w / s), s.T.copy()
 
 
-def quantize_weight_fp8(w_nk: np.ndarray) -> tuple[np.ndarray, np.float32]:
+def tensor_scale(amax: float, dtype: str = "bf16", eps: float = 1e-6) -> np.float32:
+    """``(amax / 448).clamp(min=eps).to(float32)`` evaluated by torch on a GPU tensor
+    of ``dtype`` (fp8.py:125,154-155): the product by fl32(1/448) is computed in
+    fp32 and rounded to ``dtype``, the clamp bound is ``dtype(eps)``, then the
+    value is widened to fp32.  ``amax`` is already a ``dtype`` value."""
+    v = round_to(np.array([F32(amax) * _INV_MAX], F32), dtype)[0]
+    lo = round_to(np.array([eps], F32), dtype)[0]
+    return F32(max(v, lo))
+
+
+def quantize_weight_fp8(w_nk: np.ndarray, dtype: str = "bf16") -> tuple[np.ndarray, np.float32]:
+    """Tensorwise weight quant (fp8.py:119-126) of a ``dtype`` weight held as fp32."""
     w = np.asarray(w_nk, dtype=F32)
-    s = F32(max(F32(np.abs(w).max()) / F32(E4M3_MAX), F32(1e-6)))
+    s = tensor_scale(np.abs(w).max(), dtype)
     return e4m3_encode(w / s), s
 
 
@@ -59,11 +86,13 @@ def quantize_activation_per_token(x_mk: np.ndarray) -> tuple[np.ndarray, np.ndar
     return e4m3_encode(x / s), s
 
 
-def quantize_activation_tensor(x: np.ndarray, scale: np.float32 | None = None
-                               ) -> tuple[np.ndarray, np.float32]:
+def quantize_activation_tensor(x: np.ndarray, scale: np.float32 | None = None,
+                               dtype: str = "bf16") -> tuple[np.ndarray, np.float32]:
+    """Tensorwise activation quant (fp8.py:141-181) of a ``dtype`` tensor held as fp32:
+    dynamic scale as ``tensor_scale`` unless given, then ``x * (1/s)`` -> e4m3."""
     x = np.asarray(x, dtype=F32)
     if scale is None:
-        scale = F32(max(F32(np.abs(x).max()) / F32(E4M3_MAX), F32(1e-6)))
+        scale = tensor_scale(np.abs(x).max(), dtype)
     inv = F32(F32(1.0) / F32(scale))
     return e4m3_encode(x * inv), F32(scale)
 

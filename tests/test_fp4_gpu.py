@@ -159,67 +159,3 @@ def test_mxfp4_moe_matches_oracle(dev, monkeypatch, t, k, kind):
     ref = omoe.moe_reference(x.float().cpu().numpy(), w.cpu().numpy(), ids.cpu().numpy(), experts,
                              linear=omoe.mxfp4_linear)
     assert _rel_err(y.float().cpu().numpy(), ref) <= TOL
-
-
-def test_moe_forward_hook_mxfp4_matches_per_expert_loop(dev):
-    """DSv4 MoE.forward with MXFP4 experts: the fused path (prepare_fused_experts ->
-    fused_mxfp4_moe) equals the model's own per-expert loop over MXFP4 linears."""
-    import types
-    from torchinferno_amd import hooks
-    from torchinferno_amd.kernels import moe as tmoe
-
-    e, h, inter, k = 6, 256, 256, 2
-    rng = np.random.default_rng(11)
-    mod = types.ModuleType("fake_dsv4")
-    mod.linear = None
-    undo = hooks.patch_deepseek_v4_module(mod)
-
-    def q(n, kk):
-        w = torch.from_numpy(rng.integers(0, 256, (n, kk // 2), dtype=np.uint8)).to(dev).view(torch.float4_e2m1fn_x2)
-        w.scale = torch.from_numpy(rng.integers(118, 122, (n, kk // 32), dtype=np.uint8)).to(dev) \
-            .view(torch.float8_e8m0fnu)
-        return w
-
-    class Lin:
-        def __init__(self, n, kk):
-            self.weight = q(n, kk)
-            self.scale = self.weight.scale
-
-        def __call__(self, x):
-            return mod.linear(x, self.weight)
-
-    class Expert:
-        swiglu_limit = 0.0
-
-        def __init__(self):
-            self.w1, self.w3, self.w2 = Lin(inter, h), Lin(inter, h), Lin(h, inter)
-
-        def __call__(self, x, weights=None):
-            gate, up = self.w1(x).float(), self.w3(x).float()
-            y = torch.nn.functional.silu(gate) * up
-            if weights is not None:
-                y = weights * y
-            return self.w2(y.to(x.dtype))
-
-    class Gate:
-        def __init__(self):
-            self.weight = torch.randn((e, h), device=dev)
-
-        def __call__(self, x, ids):
-            return tmoe.route_topk(x.float() @ self.weight.t(), k)
-
-    class MoE:
-        pass
-
-    try:
-        m = object.__new__(MoE)
-        m.dim, m.n_routed_experts, m.experts_start_idx, m.experts_end_idx = h, e, 0, e
-        m.gate, m.experts, m.shared_experts = Gate(), [Expert() for _ in range(e)], Expert()
-        x = torch.randn((2, 9, h), device=dev).to(torch.bfloat16)
-        loop = hooks.moe_forward(m, x, torch.zeros((2, 9), dtype=torch.long, device=dev))
-        assert hooks.prepare_fused_fp8_experts(m)
-        assert isinstance(m._ti_fused_experts, tmoe.PreparedMxfp4Experts)
-        fused = hooks.moe_forward(m, x, torch.zeros((2, 9), dtype=torch.long, device=dev))
-        torch.testing.assert_close(fused.float(), loop.float(), atol=2e-2, rtol=2e-2)
-    finally:
-        undo()

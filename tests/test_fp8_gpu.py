@@ -14,6 +14,7 @@ import torch
 
 from oracle import fp8 as ofp8
 from oracle.numerics import bf16_round
+from tests._tol import abs_codes, elementwise_ratio
 
 pytestmark = pytest.mark.gpu
 
@@ -141,6 +142,76 @@ def test_tensor_quant_bit_exact(dev):
     assert np.array_equal(_codes(xq), oq)
 
 
+def _all_positive(dtype):
+    top = 0x7F80 if dtype == torch.bfloat16 else 0x7C00
+    return torch.arange(1, top, dtype=torch.int32).to(torch.int16).view(dtype)
+
+
+@pytest.mark.parametrize("dtype,name", [(torch.bfloat16, "bf16"), (torch.float16, "fp16")])
+def test_tensor_scale_rule_is_torch_on_gpu(dev, dtype, name):
+    """Pins oracle.fp8.tensor_scale against torch's own evaluation of fp8.py:125 on the
+    GPU (the reference runs it on its weight's / activation's device) for every finite
+    positive amax of the dtype, and the per-channel rule (fp8.py:131-134, fp32) for every
+    bf16 amax: torch turns division by a host scalar into a reciprocal multiply."""
+    v = _all_positive(dtype).to(dev)
+    gpu = (v / 448.0).clamp(min=1e-6).to(torch.float32).cpu().numpy()
+    orc = np.array([ofp8.tensor_scale(a, name) for a in v.float().cpu().numpy()], np.float32)
+    assert np.array_equal(gpu.view(np.uint32), orc.view(np.uint32))
+    if dtype == torch.bfloat16:
+        w = torch.zeros((v.numel(), 8), dtype=dtype, device=dev)
+        w[:, 3] = -v
+        ch = (w.abs().amax(dim=1, keepdim=True).to(torch.float32) / 448.0).clamp(min=1e-10)
+        _, os_ = ofp8.quantize_weight_fp8_per_channel(w.float().cpu().numpy())
+        assert np.array_equal(ch.cpu().numpy()[:, 0].view(np.uint32), os_[0].view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype,name", [(torch.bfloat16, "bf16"), (torch.float16, "fp16")])
+@pytest.mark.parametrize("scale", [0.02, 1.0, 2e-6])
+def test_tensorwise_weight_quant_bit_exact(dev, dtype, name, scale):
+    """quantize_weight_fp8 (fp8.py:119-126): scale and codes equal the oracle."""
+    from torchinferno_amd.kernels import fp8 as tf8
+    g = torch.Generator().manual_seed(int(scale * 1e6) + 3)
+    w = (torch.randn((257, 384), generator=g) * scale).to(dtype)
+    wq, ws = tf8.quantize_weight_fp8(w.to(dev))
+    oq, os_ = ofp8.quantize_weight_fp8(w.float().numpy(), name)
+    assert ws.dtype == torch.float32 and ws.item() == os_
+    assert np.array_equal(_codes(wq), oq)
+
+
+@pytest.mark.parametrize("dtype,name", [(torch.bfloat16, "bf16"), (torch.float16, "fp16")])
+@pytest.mark.parametrize("m,k,scale", [(1, 128, 1.0), (32, 128, 1.0), (300, 1000, 7.0), (64, 8192, 1e-3)])
+def test_dynamic_tensor_activation_quant_bit_exact(dev, dtype, name, m, k, scale):
+    """quantize_activation_fp8(x) with scale=None (fp8.py:141-181): the dynamic scale and
+    the codes equal the oracle bit for bit."""
+    from torchinferno_amd.kernels import fp8 as tf8
+    g = torch.Generator().manual_seed(m + k)
+    x = (torch.randn((m, k), generator=g) * scale).to(dtype)
+    xq, xs = tf8.quantize_activation_fp8(x.to(dev))
+    oq, os_ = ofp8.quantize_activation_tensor(x.float().numpy(), None, name)
+    assert xs.item() == os_
+    assert np.array_equal(_codes(xq), oq)
+
+
+def test_block_act_quant_unaligned_output(dev):
+    """A 16-byte aligned input with an output only 2-byte aligned (a C caller's carved
+    buffer) takes the 4-byte-access kernel; codes and scales equal the oracle."""
+    from torchinferno_amd import _lib
+    m, k = 5, 640
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn((m, k), generator=g) * 2).to(torch.bfloat16)
+    xd = x.to(dev)
+    buf = torch.zeros(m * k + 16, dtype=torch.uint8, device=dev)
+    xq = buf[2:2 + m * k]
+    assert xd.data_ptr() % 16 == 0 and xq.data_ptr() % 8 == 2
+    xs = torch.empty((m, k // 128), dtype=torch.float32, device=dev)
+    _lib.call("ti_fp8_quant_block", xd.data_ptr(), _lib.dtype_code(xd.dtype), m, k, 128, 0,
+              xq.data_ptr(), xs.data_ptr(), 0, _lib.stream_of(xd))
+    oq, os_ = ofp8.act_quant_block(x.float().numpy())
+    assert np.array_equal(xq.view(m, k).cpu().numpy(), oq)
+    assert np.array_equal(xs.cpu().numpy().view(np.uint32), os_.view(np.uint32))
+    assert int(buf[:2].sum()) == 0 and int(buf[2 + m * k:].sum()) == 0
+
+
 def test_static_activation_scale_reference_case(dev):
     """tests/test_conversion_and_kernels.py:186-205: a reusable static scale (4x margin)
     and its inverse; the op writes the caller's buffer, returns the caller's scale,
@@ -203,9 +274,14 @@ def _check_rowcol(out, xq, xs, wq, ws, rng, rows_cap=64, cols_cap=512):
     cols = _sample(out.shape[1], cols_cap, rng)
     ri = torch.as_tensor(rows, device=out.device)
     ci = torch.as_tensor(cols, device=out.device)
-    ref = ofp8.fp8_linear_rowcol(_codes(xq[ri]), xs[ri].cpu().numpy(), _codes(wq[ci]),
-                                 ws[:, ci].cpu().numpy())
+    a, b = _codes(xq[ri]), _codes(wq[ci])
+    sa, sb = xs[ri].cpu().numpy(), ws[:, ci].cpu().numpy()
+    ref = ofp8.fp8_linear_rowcol(a, sa, b, sb)
     got = out[ri][:, ci].float().cpu().numpy()
+    # elementwise: 1 ulp of the 16-bit output + 2^-16 of the sum of |terms|
+    ulps = 1.0 if out.dtype == torch.bfloat16 else 1.0 / 8  # fp16 ulp = bf16 ulp / 8
+    ratio = elementwise_ratio(got, ref, ofp8.fp8_linear_rowcol(abs_codes(a), sa, abs_codes(b), sb), ulps)
+    assert ratio <= 1.0, ratio
     return _rel_err(got, ref)
 
 
@@ -343,12 +419,17 @@ def _check_block(out, a, a_s, b, b_s, rng, rows_cap=32, cols_cap=384):
     b_sub = _codes(b[ci])
     a_sub = _codes(a[ri])
     ref = np.zeros((len(rows), len(cols)), np.float32)
+    ref_abs = np.zeros_like(ref)
     # one oracle call per distinct column block (its b_s row applies to all its columns)
     for blk in np.unique(cols // 128):
         sel = np.nonzero(cols // 128 == blk)[0]
         ref[:, sel] = ofp8.fp8_gemm_block(a_sub, a_s[ri].cpu().numpy(), b_sub[sel],
                                           bs_rows[sel[:1]].reshape(1, -1))
+        ref_abs[:, sel] = ofp8.fp8_gemm_block(abs_codes(a_sub), a_s[ri].cpu().numpy(), abs_codes(b_sub[sel]),
+                                              bs_rows[sel[:1]].reshape(1, -1))
     got = out[ri][:, ci].float().cpu().numpy()
+    ratio = elementwise_ratio(got, ref, ref_abs)
+    assert ratio <= 1.0, ratio
     return _rel_err(got, ref)
 
 

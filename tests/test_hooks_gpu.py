@@ -2,7 +2,6 @@
 linear/MoE hooks run this package's kernels, keep the reference's contracts
 (lazy per-key cache, caller-owned out, M gates, sticky failure -> None), and the
 custom ops pass torch.library.opcheck."""
-import types
 
 import numpy as np
 import pytest
@@ -102,81 +101,6 @@ def test_fp8_decode_static_scale(dev, layer, monkeypatch):
     assert y.shape == (16, 1, 256)
     assert layer._fp8_gu_decode_activation_scale.numel() == 1  # cached static scale (margin 4)
     torch.testing.assert_close(y.float(), (x.float() @ w.float().t()), atol=1.0, rtol=0.3)
-
-
-def test_deepseek_linear_and_moe_hooks(dev):
-    from torchinferno_amd import hooks
-    from torchinferno_amd.kernels import block_fp8 as tb
-    mod = types.ModuleType("fake_dsv4")
-    mod.linear = None
-    undo = hooks.patch_deepseek_v4_module(mod)
-    try:
-        g = torch.Generator(device=dev).manual_seed(4)
-        w = (torch.randn((256, 512), generator=g, device=dev) * 0.02)
-        wq = w.to(torch.float8_e4m3fn)  # unit block scales
-        wq.scale = torch.ones((2, 4), device=dev)
-        x = torch.randn((3, 5, 512), generator=g, device=dev).to(torch.bfloat16)
-        y = mod.linear(x, wq)
-        xq, xs = tb.act_quant(x)
-        assert torch.equal(y, tb.fp8_gemm(xq, xs, wq, wq.scale))
-    finally:
-        undo()
-
-
-def test_moe_forward_hook_matches_per_expert_loop(dev):
-    """MoE.forward with fused experts equals its own per-expert loop (built from the
-    same block-FP8 linears)."""
-    from torchinferno_amd import hooks
-    from torchinferno_amd.kernels import block_fp8 as tb
-    from torchinferno_amd.kernels import moe as tmoe
-
-    e, h, inter, k = 6, 256, 256, 2
-    g = torch.Generator(device=dev).manual_seed(7)
-
-    def q(n, kk):
-        w = (torch.randn((n, kk), generator=g, device=dev) * 0.02).to(torch.float8_e4m3fn)
-        w.scale = torch.rand((n // 128, kk // 128), generator=g, device=dev) + 0.5
-        return w
-
-    class Lin:
-        def __init__(self, n, kk):
-            self.weight = q(n, kk)
-            self.scale = self.weight.scale
-
-        def __call__(self, x):
-            return tb.linear(x, self.weight, self.scale)
-
-    class Expert:
-        swiglu_limit = 0.0
-
-        def __init__(self):
-            self.w1, self.w3, self.w2 = Lin(inter, h), Lin(inter, h), Lin(h, inter)
-
-        def __call__(self, x, weights=None):
-            gate, up = self.w1(x).float(), self.w3(x).float()
-            y = torch.nn.functional.silu(gate) * up
-            if weights is not None:
-                y = weights * y
-            return self.w2(y.to(x.dtype))
-
-    class Gate:
-        def __init__(self):
-            self.weight = torch.randn((e, h), generator=g, device=dev)
-
-        def __call__(self, x, ids):
-            return tmoe.route_topk(x.float() @ self.weight.t(), k)
-
-    class MoE:
-        pass
-
-    m = object.__new__(MoE)
-    m.dim, m.n_routed_experts, m.experts_start_idx, m.experts_end_idx = h, e, 0, e
-    m.gate, m.experts, m.shared_experts = Gate(), [Expert() for _ in range(e)], Expert()
-    x = torch.randn((2, 9, h), generator=g, device=dev).to(torch.bfloat16)
-    loop = hooks.moe_forward(m, x, torch.zeros((2, 9), dtype=torch.long, device=dev))
-    assert hooks.prepare_fused_fp8_experts(m)
-    fused = hooks.moe_forward(m, x, torch.zeros((2, 9), dtype=torch.long, device=dev))
-    torch.testing.assert_close(fused.float(), loop.float(), atol=2e-2, rtol=2e-2)
 
 
 def test_custom_ops_opcheck(dev):

@@ -39,14 +39,84 @@ def test_per_channel_scale_closed_form():
     rng = np.random.default_rng(0)
     w = rng.standard_normal((5, 64)).astype(F32)
     q, s = ofp8.quantize_weight_fp8_per_channel(w)
-    np.testing.assert_array_equal(s[0], (np.abs(w).max(1) / F32(448)).astype(F32))
+    amax = np.abs(w).max(1)
+    # the reciprocal product lies within one ulp of the quotient
+    assert np.all(np.abs(s[0].astype(np.float64) - amax / 448.0) <= np.spacing(s[0]))
+    np.testing.assert_array_equal(s[0], (amax * (F32(1) / F32(448))).astype(F32))
     # each row's absmax element encodes as +-448 (code 0x7E / 0xFE)
     idx = np.abs(w).argmax(1)
     assert all((q[r, idx[r]] & 0x7F) == 0x7E for r in range(5))
-    # matches torch's own formula on the host (library cast)
+    # codes: torch's own cast of w / s on the host (library cast)
     wt = torch.from_numpy(w)
-    ts = (wt.abs().amax(1, keepdim=True) / 448.0).clamp(min=1e-10)
-    assert np.array_equal((wt / ts).to(torch.float8_e4m3fn).view(torch.uint8).numpy(), q)
+    assert np.array_equal((wt / torch.from_numpy(s.T.copy())).to(torch.float8_e4m3fn).view(torch.uint8).numpy(), q)
+
+
+def _all_positive(dtype):
+    top = 0x7F80 if dtype == torch.bfloat16 else 0x7C00
+    return torch.arange(1, top, dtype=torch.int32).to(torch.int16).view(dtype)
+
+
+def test_tensor_scale_bf16_exhaustive_vs_torch():
+    """fp8.py:125 evaluated by torch on every finite positive bf16 amax: the scale is
+    rounded to bf16 before the clamp and the fp32 cast.  (For bf16 the quotient and
+    the reciprocal product round to the same bf16 for every input, so torch's host
+    division pins the oracle here exactly.)"""
+    v = _all_positive(torch.bfloat16)
+    want = (v / 448.0).clamp(min=1e-6).to(torch.float32).numpy()
+    got = np.array([ofp8.tensor_scale(a, "bf16") for a in v.float().numpy()], F32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_tensor_scale_fp16_vs_torch_host():
+    """Every finite positive fp16 amax: the oracle equals torch's host expression except
+    where the fp16-rounded quotient and reciprocal product differ -- there it takes the
+    product, the GPU's rule (pinned on the device in tests/test_fp8_gpu.py)."""
+    v = _all_positive(torch.float16)
+    host = (v / 448.0).clamp(min=1e-6).to(torch.float32).numpy()
+    got = np.array([ofp8.tensor_scale(a, "fp16") for a in v.float().numpy()], F32)
+    f = v.float()
+    quot = (f / 448.0).half()
+    prod = (f * (torch.tensor(1.0) / torch.tensor(448.0))).half()
+    split = (quot != prod).numpy()
+    assert 0 < split.sum() < 100
+    assert np.array_equal(got[~split], host[~split])
+    assert np.array_equal(got[split], prod.clamp(min=1e-6).float().numpy()[split])
+
+
+def test_tensor_scale_is_not_fp32_arithmetic():
+    """A fp32 scale (no rounding to the input dtype) is the plausible mistake: on this
+    bf16 amax it gives 0.02748326, the reference's arithmetic 0.02746582."""
+    amax = F32(12.3125)  # a bf16 value
+    assert ofp8.tensor_scale(amax, "bf16") == F32(0.02746582)
+    assert F32(amax / F32(448)) != ofp8.tensor_scale(amax, "bf16")
+    assert ofp8.tensor_scale(F32(1e-7), "bf16") == torch.tensor(1e-6, dtype=torch.bfloat16).float().item()
+
+
+def test_tensorwise_weight_quant_vs_torch_host():
+    """quantize_weight_fp8 (fp8.py:119-126) on seeded bf16 weights: scale and codes equal
+    torch's own expression (bf16 amax/448 -> clamp -> fp32; fp32 quotient -> e4m3)."""
+    g = torch.Generator().manual_seed(7)
+    for scale in (0.02, 1.0, 3e-5):
+        w = (torch.randn((48, 80), generator=g) * scale).to(torch.bfloat16)
+        ws = (w.abs().amax() / 448.0).clamp(min=1e-6).to(torch.float32)
+        wq = (w.to(torch.float32) / ws).to(torch.float8_e4m3fn)
+        q, s = ofp8.quantize_weight_fp8(w.float().numpy(), "bf16")
+        assert s == ws.item()
+        assert np.array_equal(q, wq.view(torch.uint8).numpy())
+
+
+def test_dynamic_tensor_activation_quant_vs_torch_host():
+    """quantize_activation_fp8(x) with scale=None (fp8.py:154-155, cast kernel :43-51):
+    bf16 and fp16 inputs, scale and codes vs torch's expression on the host."""
+    g = torch.Generator().manual_seed(8)
+    for dt, name in ((torch.bfloat16, "bf16"), (torch.float16, "fp16")):
+        x = (torch.randn((33, 96), generator=g) * 5).to(dt)
+        sc = (x.abs().amax() / 448.0).clamp(min=1e-6).to(torch.float32)
+        inv = sc.reciprocal()
+        want = (x.to(torch.float32) * inv).to(torch.float8_e4m3fn)
+        q, s = ofp8.quantize_activation_tensor(x.float().numpy(), None, name)
+        assert s == sc.item()
+        assert np.array_equal(q, want.view(torch.uint8).numpy())
 
 
 def test_per_token_zero_row_floor():

@@ -84,3 +84,39 @@ def test_moe_permutation_equivariance_and_missing_routes():
     y2 = omoe.moe_reference(x, w, ids2, experts)
     only = omoe.moe_reference(x[:1], w[:1, :1], ids[:1, :1], experts)
     np.testing.assert_array_equal(y2[0], only[0])
+
+
+def test_expert_clamp_limit_matches_fp64_math():
+    """swiglu_limit (tensor_parallel.py:796-800): up clamped to [-l, l], gate to <= l.
+    With l small the clamp is active on most elements; the fp64 restatement agrees and
+    the unclamped expert does not."""
+    rng = np.random.default_rng(5)
+    h, inter, lim = 256, 128, 0.3
+    (w13, s13, w2, s2), = _experts(rng, 1, h, inter)
+    x = bf16_round(rng.standard_normal((3, h)).astype(F32))
+    rw = np.ones((3, 1), F32)
+    got = omoe.expert_forward(x, rw, w13, s13, w2, s2, clamp_limit=lim)
+    W13 = ofp8.dequantize_block_fp8(w13, s13).astype(np.float64)
+    W2 = ofp8.dequantize_block_fp8(w2, s2).astype(np.float64)
+    gu = x.astype(np.float64) @ W13.T
+    g, u = np.minimum(gu[:, :inter], lim), np.clip(gu[:, inter:], -lim, lim)
+    want = ((g / (1 + np.exp(-g))) * u) @ W2.T
+    assert np.abs(got - want).max() <= 0.08 * np.abs(want).max()
+    free = omoe.expert_forward(x, rw, w13, s13, w2, s2)
+    assert np.abs(free - want).max() > 0.5 * np.abs(want).max()
+
+
+def test_ue8m0_linear_uses_power_of_two_activation_scales():
+    """scale_fmt "ue8m0": the activation scales are 2^ceil(log2(amax/448)); the linear
+    stays within quantization error of the fp64 product and differs from the plain one."""
+    rng = np.random.default_rng(6)
+    (w13, s13, _, _), = _experts(rng, 1, 256, 128)
+    x = bf16_round(rng.standard_normal((5, 256)).astype(F32))
+    pow2 = omoe.ue8m0(omoe.block_fp8_linear)(x, w13, s13)
+    plain = omoe.block_fp8_linear(x, w13, s13)
+    want = x.astype(np.float64) @ ofp8.dequantize_block_fp8(w13, s13).astype(np.float64).T
+    assert np.abs(pow2 - want).max() <= 0.05 * np.abs(want).max()
+    assert not np.array_equal(pow2, plain)
+    xq, xs = ofp8.act_quant_block(x, round_scale=True)
+    assert np.array_equal(pow2, bf16_round(ofp8.fp8_gemm_block(xq, xs, w13, s13)))
+    assert np.all(np.log2(xs) == np.round(np.log2(xs)))

@@ -42,6 +42,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ti_w4a16_gemm": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ti_w4a16_plan_name": (_i, [_i, _i, _i, _i, ctypes.c_char_p, _sz]),
     "ti_fp8_quant_per_token": (_i, [_vp, _i, _i, _i, _f, _vp, _vp, _vp]),
+    "ti_fp8_quant_weight_per_channel": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "ti_fp8_quant_block": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp]),
     "ti_fp8_e4m3_selfcheck": (_i, [_vp, _vp]),
     "ti_bf16_round_selfcheck": (_i, [_vp, _vp]),
@@ -56,8 +57,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ti_fp4_scale_stepmajor": (_i, [_vp, _i, _i, _vp, _vp]),
     "ti_moe_route_topk": (_i, [_vp, _i, _i, _i, _i, _f, _vp, _vp, _vp]),
     "ti_fp8_moe_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
-    "ti_fp8_moe": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _sz, _vp]),
-    "ti_fp4_moe": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp, _vp, _sz, _vp]),
+    "ti_fp8_moe": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _i, _vp, _vp, _sz, _vp]),
+    "ti_fp4_moe": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _vp, _vp, _sz, _vp]),
 }
 
 

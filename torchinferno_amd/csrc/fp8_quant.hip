@@ -45,8 +45,11 @@ __device__ __forceinline__ uint2 pack8(const uint32_t (&c)[8]) {
                     c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24));
 }
 
-// One workgroup (256 threads) per row; K % 8 == 0.
-template <int DT>
+// One workgroup (256 threads) per row; K % 8 == 0.  RECIP forms the scale as
+// amax * fl32(1/448) -- what torch computes for ``amax.float() / 448.0`` on a GPU
+// tensor (a host-scalar divisor becomes a reciprocal multiply), the per-channel
+// weight quant of fp8.py:129-138 -- instead of the quotient amax / 448.
+template <int DT, bool RECIP>
 __global__ __launch_bounds__(256) void quant_per_token_kernel(const uint16_t* __restrict__ x, int K,
                                                               uint8_t* __restrict__ q,
                                                               float* __restrict__ s, float eps) {
@@ -64,7 +67,7 @@ __global__ __launch_bounds__(256) void quant_per_token_kernel(const uint16_t* __
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float sc = fmaxf(amax / kE4M3Max, eps);
+  const float sc = fmaxf(RECIP ? amax * (1.0f / kE4M3Max) : amax / kE4M3Max, eps);
   if (threadIdx.x == 0) s[row] = sc;
   uint8_t* qr = q + row * K;
   for (int i = threadIdx.x * 8; i < K; i += 256 * 8) {
@@ -414,22 +417,34 @@ extern "C" int ti_bf16_round_selfcheck(unsigned long long* counts, hipStream_t s
   return TI_OK;
 }
 
+static int quant_rows(const char* who, bool recip, const void* x, int x_dtype, int M, int K, float eps,
+                      uint8_t* xq, float* xs, hipStream_t stream) {
+  TI_CHECK_ARG(x && xq && xs, "%s: null pointer", who);
+  TI_CHECK_ARG(act_dtype_ok(x_dtype), "%s: input must be fp16 or bf16", who);
+  TI_CHECK_SHAPE(M >= 0 && K > 0 && K % 8 == 0, "%s: need K %% 8 == 0 (K=%d)", who, K);
+  TI_CHECK_ARG(((uintptr_t)x & 15) == 0 && ((uintptr_t)xq & 7) == 0,
+               "%s: input must be 16-byte and output 8-byte aligned", who);
+  if (M == 0) return TI_OK;
+#define TI_QR(DT, R) \
+  hipLaunchKernelGGL((quant_per_token_kernel<DT, R>), dim3(M), dim3(256), 0, stream, (const uint16_t*)x, K, xq, xs, eps)
+  if (x_dtype == TI_DTYPE_F16) {
+    if (recip) TI_QR(TI_DTYPE_F16, true); else TI_QR(TI_DTYPE_F16, false);
+  } else {
+    if (recip) TI_QR(TI_DTYPE_BF16, true); else TI_QR(TI_DTYPE_BF16, false);
+  }
+#undef TI_QR
+  TI_CHECK_LAUNCH(who);
+  return TI_OK;
+}
+
 extern "C" int ti_fp8_quant_per_token(const void* x, int x_dtype, int M, int K, float eps,
                                       uint8_t* xq, float* xs, hipStream_t stream) {
-  TI_CHECK_ARG(x && xq && xs, "ti_fp8_quant_per_token: null pointer");
-  TI_CHECK_ARG(act_dtype_ok(x_dtype), "ti_fp8_quant_per_token: x must be fp16 or bf16");
-  TI_CHECK_SHAPE(M >= 0 && K > 0 && K % 8 == 0, "ti_fp8_quant_per_token: need K %% 8 == 0 (K=%d)", K);
-  TI_CHECK_ARG(((uintptr_t)x & 15) == 0 && ((uintptr_t)xq & 7) == 0,
-               "ti_fp8_quant_per_token: x must be 16-byte and xq 8-byte aligned");
-  if (M == 0) return TI_OK;
-  if (x_dtype == TI_DTYPE_F16)
-    hipLaunchKernelGGL(quant_per_token_kernel<TI_DTYPE_F16>, dim3(M), dim3(256), 0, stream,
-                       (const uint16_t*)x, K, xq, xs, eps);
-  else
-    hipLaunchKernelGGL(quant_per_token_kernel<TI_DTYPE_BF16>, dim3(M), dim3(256), 0, stream,
-                       (const uint16_t*)x, K, xq, xs, eps);
-  TI_CHECK_LAUNCH("ti_fp8_quant_per_token");
-  return TI_OK;
+  return quant_rows("ti_fp8_quant_per_token", false, x, x_dtype, M, K, eps, xq, xs, stream);
+}
+
+extern "C" int ti_fp8_quant_weight_per_channel(const void* w, int w_dtype, int N, int K, uint8_t* wq,
+                                               float* ws, hipStream_t stream) {
+  return quant_rows("ti_fp8_quant_weight_per_channel", true, w, w_dtype, N, K, 1e-10f, wq, ws, stream);
 }
 
 extern "C" int ti_fp8_quant_block(const void* x, int x_dtype, int M, int K, int block_size,

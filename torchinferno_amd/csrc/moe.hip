@@ -224,7 +224,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const int* __restr
 }
 
 // h = bf16(w * silu(g) * u) over one sorted row's 128-wide block, then 1x128
-// e4m3 quant (act_quant).  One wave per (row, four blocks); rows past the
+// e4m3 quant (act_quant; power-of-two scales when round_scale).  One wave per (row, four blocks); rows past the
 // routed count are skipped.
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __restrict__ gu, int I,
                                                            const float* __restrict__ route_w,
@@ -232,8 +232,8 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
                                                            const int* __restrict__ num_rows_tiles,
                                                            const int* __restrict__ tile_row0,
                                                            const int* __restrict__ tile_rows, long R,
-                                                           float clamp_limit, uint8_t* __restrict__ hq,
-                                                           float* __restrict__ hs) {
+                                                           float clamp_limit, int round_scale,
+                                                           uint8_t* __restrict__ hq, float* __restrict__ hs) {
   // One wave per (row, four 128-wide blocks); each 16-lane group owns a block,
   // 8 elements (16-byte loads) per lane.
   const int lane = threadIdx.x & 63;
@@ -272,7 +272,12 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
 #pragma unroll
   for (int o = 1; o < 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
   amax = fmaxf(amax, 1e-4f);
-  const float s = amax * (1.0f / kE4M3Max);
+  float s = amax * (1.0f / kE4M3Max);
+  if (round_scale) {  // 2^ceil(log2(amax / 448)), the ue8m0 scale format
+    const uint32_t b = __float_as_uint(s);
+    const int e = (int)((b >> 23) & 0xFF) - 127 + ((b & 0x7FFFFFu) != 0 ? 1 : 0);
+    s = __uint_as_float((uint32_t)(e + 127) << 23);
+  }
   float y[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) y[i] = fminf(fmaxf(h[i] / s, -kE4M3Max), kE4M3Max);
@@ -359,8 +364,8 @@ extern "C" size_t ti_fp8_moe_workspace_bytes(int T, int k, int E, int H, int I) 
 // 32 K) weight formats; activations are 1x128 block FP8 in both.
 static int moe_run(const char* name, int smode, int sb_layout, const void* hidden, const float* topk_weights,
                    const int32_t* topk_ids, int T, int k, const uint8_t* w13, const void* s13, const uint8_t* w2,
-                   const void* s2, int E, int H, int I, float clamp_limit, void* out, void* workspace,
-                   size_t workspace_bytes, hipStream_t stream) {
+                   const void* s2, int E, int H, int I, float clamp_limit, int round_scale, void* out,
+                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
   TI_CHECK_ARG(hidden && topk_weights && topk_ids && w13 && s13 && w2 && s2 && out, "%s: null pointer", name);
   TI_CHECK_SHAPE(moe_shape_ok(T, k, E, H, I),
                  "%s: need H %% 128 == 0, I %% 128 == 0, 1 <= k <= 16, E <= 1024 (T=%d k=%d E=%d H=%d I=%d)",
@@ -381,7 +386,7 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
   const bool f4 = smode == 2;
 
   // 1. hidden -> e4m3 1x128
-  int st = ti_fp8_quant_block(hidden, TI_DTYPE_BF16, T, H, 128, 0, w.xq, w.xs, 0, stream);
+  int st = ti_fp8_quant_block(hidden, TI_DTYPE_BF16, T, H, 128, round_scale ? 1 : 0, w.xq, w.xs, 0, stream);
   if (st != TI_OK) return st;
   // 2. align
   hipLaunchKernelGGL(align_kernel, dim3(1), dim3(kAlignThreads), 0, stream, (const int*)topk_ids, (int)R, E, p.bm,
@@ -405,8 +410,8 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
   // 4. swiglu x route weight -> 1x128 quant
   const long items = R * ((I / 128 + 3) / 4);
   hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, w.out1, I,
-                     topk_weights, w.route_of_pos, w.num_tiles, w.tile_row0, w.tile_rows, R, clamp_limit, w.hq,
-                     w.hs);
+                     topk_weights, w.route_of_pos, w.num_tiles, w.tile_row0, w.tile_rows, R, clamp_limit,
+                     round_scale, w.hq, w.hs);
   TI_CHECK_LAUNCH("moe(swiglu)");
   // 5. grouped w2: [R, H] = hq . w2[e]^T
   fp8::GemmArgs g2 = g;
@@ -428,17 +433,17 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
 
 extern "C" int ti_fp8_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids, int T, int k,
                           const uint8_t* w13, const float* s13, const uint8_t* w2, const float* s2, int E, int H,
-                          int I, float clamp_limit, void* out, void* workspace, size_t workspace_bytes,
-                          hipStream_t stream) {
-  return moe_run("ti_fp8_moe", 1, 0, hidden, topk_weights, topk_ids, T, k, w13, s13, w2, s2, E, H, I, clamp_limit, out,
-                 workspace, workspace_bytes, stream);
+                          int I, float clamp_limit, int round_scale, void* out, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream) {
+  return moe_run("ti_fp8_moe", 1, 0, hidden, topk_weights, topk_ids, T, k, w13, s13, w2, s2, E, H, I, clamp_limit,
+                 round_scale, out, workspace, workspace_bytes, stream);
 }
 
 extern "C" int ti_fp4_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids, int T, int k,
                           const uint8_t* w13, const uint8_t* s13, const uint8_t* w2, const uint8_t* s2,
-                          int scale_layout, int E, int H, int I, float clamp_limit, void* out, void* workspace,
-                          size_t workspace_bytes, hipStream_t stream) {
+                          int scale_layout, int E, int H, int I, float clamp_limit, int round_scale, void* out,
+                          void* workspace, size_t workspace_bytes, hipStream_t stream) {
   TI_CHECK_ARG(scale_layout == 0 || scale_layout == 1, "ti_fp4_moe: scale_layout must be 0 or 1");
-  return moe_run("ti_fp4_moe", 2, scale_layout, hidden, topk_weights, topk_ids, T, k, w13, s13, w2, s2, E, H, I, clamp_limit, out,
-                 workspace, workspace_bytes, stream);
+  return moe_run("ti_fp4_moe", 2, scale_layout, hidden, topk_weights, topk_ids, T, k, w13, s13, w2, s2, E, H, I,
+                 clamp_limit, round_scale, out, workspace, workspace_bytes, stream);
 }

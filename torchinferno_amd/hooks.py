@@ -23,6 +23,7 @@ Nothing here imports the reference: callers pass the class / module objects.
 from __future__ import annotations
 
 import os
+import sys
 import types
 import warnings
 from typing import Callable
@@ -281,17 +282,29 @@ def patch_fused_producers(module: types.ModuleType) -> Callable[[], None]:
 # --------------------------------------------------------------------------- DeepSeek-V4
 
 
-def deepseek_linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+def deepseek_linear(x: Tensor, weight: Tensor, bias: Tensor | None = None, *,
+                    scale_fmt: str | None = None, scale_dtype: torch.dtype = torch.float32) -> Tensor:
     """DSv4 ``linear`` (tensor_parallel.py:195-207): e4m3 weights (``.scale``
     per 128x128 block) and MXFP4 weights (``float4_e2m1fn_x2``, ``.scale`` one
-    E8M0 per 32 K) run act_quant + the block-FP8 / FP4 GEMM here; other dtypes
-    keep ``F.linear``."""
+    E8M0 per 32 K) run ``act_quant(x, 128, scale_fmt, scale_dtype)`` + the
+    block-FP8 / FP4 GEMM here; other dtypes keep ``F.linear``.  ``scale_fmt`` and
+    ``scale_dtype`` are the model module's globals (set in ``MoE.__init__`` /
+    the checkpoint path, tensor_parallel.py:1199-1212,1641);
+    ``patch_deepseek_v4_module`` passes them at call time."""
     from .kernels import block_fp8
 
     assert bias is None
     if weight.dtype in (torch.float8_e4m3fn, torch.float4_e2m1fn_x2):
-        return block_fp8.linear(x, weight, weight.scale)
+        return block_fp8.linear(x, weight, weight.scale, scale_fmt, scale_dtype)
     return torch.nn.functional.linear(x, weight)
+
+
+def _module_scale_format(module: types.ModuleType | None) -> tuple[str | None, torch.dtype]:
+    """The reference module's ``scale_fmt`` / ``scale_dtype`` globals as they are now
+    (the model sets them after import, tensor_parallel.py:1199-1212)."""
+    if module is None:
+        return None, torch.float32
+    return getattr(module, "scale_fmt", None), getattr(module, "scale_dtype", torch.float32)
 
 
 def prepare_fused_fp8_experts(moe_module) -> bool:
@@ -329,8 +342,10 @@ def moe_forward(self, x: Tensor, input_ids: Tensor) -> Tensor:
     fused = getattr(self, "_ti_fused_experts", None)
     if fused is not None:
         run = _moe.fused_mxfp4_moe if isinstance(fused, _moe.PreparedMxfp4Experts) else _moe.fused_fp8_moe
+        scale_fmt, _ = _module_scale_format(sys.modules.get(type(self).__module__))
         y = run(x.contiguous(), weights.float().contiguous(), indices.int().contiguous(), fused,
-                clamp_limit=float(getattr(self.shared_experts, "swiglu_limit", 0.0) or 0.0))
+                clamp_limit=float(getattr(self.shared_experts, "swiglu_limit", 0.0) or 0.0),
+                scale_fmt=scale_fmt)
         y = y.float()
     else:
         y = torch.zeros_like(x, dtype=torch.float32)
@@ -351,7 +366,12 @@ def patch_deepseek_v4_module(module: types.ModuleType, moe_cls: type | None = No
     """Replace ``module.linear`` (which ``Linear.forward`` looks up at call time) and,
     if given, ``moe_cls.forward`` / ``moe_cls.prepare_fused_experts``.  Returns undo."""
     saved_linear = module.linear
-    module.linear = deepseek_linear
+
+    def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+        scale_fmt, scale_dtype = _module_scale_format(module)
+        return deepseek_linear(x, weight, bias, scale_fmt=scale_fmt, scale_dtype=scale_dtype)
+
+    module.linear = linear
     saved_moe = {}
     if moe_cls is not None:
         saved_moe = {n: moe_cls.__dict__.get(n) for n in ("forward", "prepare_fused_experts")}

@@ -8,8 +8,11 @@ power-of-two ceiling when ``scale_fmt`` is set), ``y = clamp(x / s, +-448)``.
 bf16 out.  ``fp4_gemm(a, a_s, b, b_s)``: FP8 activations x MXFP4 weights
 (deepseek_v4_tilelang_definitions.py:674-769): ``b`` e2m1 ``[N, K/2]``, ``b_s`` one
 E8M0 scale per 32 K (``float8_e8m0fnu``, or fp32 powers of two).  All run
-libti_quant.so's gfx950 kernels.  Activation scales are fp32; the reference's
-``float8_e8m0fnu`` activation-scale storage is not supported (ValueError).
+libti_quant.so's gfx950 kernels.  Block scales may be stored as fp32 or, as the
+reference's ``scale_dtype=float8_e8m0fnu`` (tensor_parallel.py:1211-1212), as
+E8M0 bytes: those are powers of two, widened to fp32 exactly before the GEMM;
+E8M0 activation scales are produced only with a ``scale_fmt`` (power-of-two
+scales), the only combination the reference model configures.
 """
 from __future__ import annotations
 
@@ -22,9 +25,33 @@ from .fp8 import FP8_E4M3, _ws_args
 BLOCK = 128
 
 
+E8M0 = torch.float8_e8m0fnu
+
+
 def _check_scale_dtype(scale_dtype: torch.dtype) -> None:
-    if scale_dtype != torch.float32:
-        raise ValueError("only fp32 block scales are supported (float8_e8m0fnu storage is not)")
+    if scale_dtype not in (torch.float32, E8M0):
+        raise ValueError("block scales must be stored as float32 or float8_e8m0fnu")
+
+
+def _f32_scales(s: Tensor) -> Tensor:
+    """fp32 view of block scales: fp32 as is, E8M0 widened (exact: powers of two)."""
+    if s.dtype == torch.float32:
+        return s
+    if s.dtype == E8M0:
+        return s.float()
+    raise ValueError("block scales must be float32 or float8_e8m0fnu")
+
+
+def _weight_scales_f32(weight: Tensor, weight_scale: Tensor) -> Tensor:
+    """``weight_scale`` as fp32, cached on the weight when it is stored as E8M0
+    (weight preparation: the conversion runs once per weight)."""
+    if weight_scale.dtype == torch.float32:
+        return weight_scale
+    cached = getattr(weight, "_ti_scale_f32", None)
+    if cached is None or cached[0] is not weight_scale:
+        cached = (weight_scale, _f32_scales(weight_scale).contiguous())
+        weight._ti_scale_f32 = cached
+    return cached[1]
 
 
 def act_quant(
@@ -43,6 +70,8 @@ def act_quant(
     if n % block_size:
         raise ValueError("FP8 quantization width must be divisible by block size")
     _check_scale_dtype(scale_dtype)
+    if scale_dtype == E8M0 and scale_fmt is None:
+        raise ValueError("float8_e8m0fnu activation scales need a scale_fmt (power-of-two scales)")
     _lib.require_device(x)
     if x.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("FP8 block quantization input must be bf16 or fp16")
@@ -56,7 +85,7 @@ def act_quant(
         deq = y.view(rows, n // block_size, block_size).float() * s.view(rows, -1, 1)
         x.copy_(deq.view(x.shape).to(x.dtype))
         return x
-    return y, s
+    return y, (s if scale_dtype == torch.float32 else s.to(E8M0))
 
 
 def fp8_gemm(
@@ -74,8 +103,9 @@ def fp8_gemm(
     _check_scale_dtype(scale_dtype)
     if a.dtype != FP8_E4M3 or b.dtype != FP8_E4M3:
         raise ValueError("FP8 GEMM operands must be float8_e4m3fn")
-    if a_s.dtype != torch.float32 or b_s.dtype != torch.float32:
-        raise ValueError("FP8 GEMM scales must be fp32")
+    if a_s.dtype != scale_dtype or b_s.dtype != scale_dtype:
+        raise ValueError("FP8 GEMM scales must have the given scale_dtype")
+    a_s, b_s = _f32_scales(a_s), _f32_scales(b_s)
     _lib.require_device(a, a_s, b, b_s)
     k = a.size(-1)
     m = a.numel() // k
@@ -100,9 +130,10 @@ def _fp8_gemm_raw(a: Tensor, a_s: Tensor, a_layout: int, b: Tensor, b_s: Tensor)
     return out
 
 
-def _act_quant_stepmajor(x: Tensor) -> tuple[Tensor, Tensor]:
+def _act_quant_stepmajor(x: Tensor, round_scale: bool = False) -> tuple[Tensor, Tensor]:
     """1x128 quant with the scales step-major, ``[K/128, rows]`` (the layout the
-    GEMMs read as one contiguous run per tile and K step)."""
+    GEMMs read as one contiguous run per tile and K step); power-of-two scales
+    when ``round_scale``."""
     _lib.require_device(x)
     if x.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("FP8 block quantization input must be bf16 or fp16")
@@ -114,8 +145,8 @@ def _act_quant_stepmajor(x: Tensor) -> tuple[Tensor, Tensor]:
     y = torch.empty(value.shape, dtype=FP8_E4M3, device=x.device)
     s = torch.empty((n // BLOCK, rows), dtype=torch.float32, device=x.device)
     if rows:
-        _lib.call("ti_fp8_quant_block", value.data_ptr(), _lib.dtype_code(value.dtype), rows, n, BLOCK, 0,
-                  y.data_ptr(), s.data_ptr(), 1, _lib.stream_of(value))
+        _lib.call("ti_fp8_quant_block", value.data_ptr(), _lib.dtype_code(value.dtype), rows, n, BLOCK,
+                  int(round_scale), y.data_ptr(), s.data_ptr(), 1, _lib.stream_of(value))
     return y, s
 
 
@@ -180,8 +211,9 @@ def fp4_gemm(
     _check_scale_dtype(scale_dtype)
     if a.dtype != FP8_E4M3 or b.dtype not in (FP4, torch.uint8):
         raise ValueError("FP4 GEMM operands must be float8_e4m3fn activations and float4_e2m1fn_x2 weights")
-    if a_s.dtype != torch.float32:
-        raise ValueError("FP4 GEMM activation scales must be fp32")
+    if a_s.dtype != scale_dtype:
+        raise ValueError("FP4 GEMM activation scales must have the given scale_dtype")
+    a_s = _f32_scales(a_s)
     _lib.require_device(a, a_s, b, b_s)
     k = a.size(-1)
     m = a.numel() // k
@@ -196,11 +228,19 @@ def fp4_gemm(
     return _fp4_gemm_raw(a, a_s, 0, b, eb, 0, n)
 
 
-def linear(x: Tensor, weight: Tensor, weight_scale: Tensor) -> Tensor:
+def linear(x: Tensor, weight: Tensor, weight_scale: Tensor, scale_fmt: str | None = None,
+           scale_dtype: torch.dtype = torch.float32) -> Tensor:
     """DeepSeek ``linear`` for an e4m3 or MXFP4 weight (src/torchinferno/models/
-    deepseek_v4/tensor_parallel.py:195-207): ``act_quant`` then ``fp8_gemm`` /
-    ``fp4_gemm``, bf16 out.  The activation scales stay internal, so they are
-    kept step-major (``[K/128, rows]``), which the GEMMs read fastest."""
+    deepseek_v4/tensor_parallel.py:195-207): ``act_quant(x, 128, scale_fmt,
+    scale_dtype)`` then ``fp8_gemm`` / ``fp4_gemm``, bf16 out.  ``scale_fmt`` set
+    ("ue8m0" on the DSv4 checkpoint path) rounds the activation scales up to powers
+    of two.  The activation scales stay internal, so they are kept fp32 and
+    step-major (``[K/128, rows]``), which the GEMMs read fastest; E8M0 storage of
+    them would hold the same powers of two."""
+    _check_scale_dtype(scale_dtype)
+    if scale_dtype == E8M0 and scale_fmt is None:
+        raise ValueError("float8_e8m0fnu activation scales need a scale_fmt (power-of-two scales)")
+    round_scale = scale_fmt is not None
     if weight.dtype == FP4:
         # The step-major copy of the weight's scales is built on first use and
         # cached on the weight (like the reference's per-layer weight caches).
@@ -213,10 +253,10 @@ def linear(x: Tensor, weight: Tensor, weight_scale: Tensor) -> Tensor:
             weight._ti_fp4_scale_stepmajor = cached
         if x.size(-1) != weight.size(1) * 2:
             raise ValueError("MXFP4 weight K does not match the activation")
-        xq, xs = _act_quant_stepmajor(x)
+        xq, xs = _act_quant_stepmajor(x, round_scale)
         return _fp4_gemm_raw(xq, xs, 1, weight, cached[1], 1, weight.size(0))
-    if weight.dtype != FP8_E4M3 or weight_scale.dtype != torch.float32:
-        raise ValueError("block-FP8 linear needs a float8_e4m3fn weight with fp32 block scales")
+    if weight.dtype != FP8_E4M3 or weight_scale.dtype not in (torch.float32, E8M0):
+        raise ValueError("block-FP8 linear needs a float8_e4m3fn weight with fp32 or E8M0 block scales")
     k = x.size(-1)
     n = weight.size(0)
     if weight.ndim != 2 or weight.size(1) != k:
@@ -224,5 +264,6 @@ def linear(x: Tensor, weight: Tensor, weight_scale: Tensor) -> Tensor:
     if tuple(weight_scale.shape) != (-(-n // BLOCK), -(-k // BLOCK)):
         raise ValueError("FP8 GEMM weight scale must be [ceil(N/128), K/128]")
     _lib.require_device(weight, weight_scale)
-    xq, xs = _act_quant_stepmajor(x)
-    return _fp8_gemm_raw(xq, xs, 1, weight.contiguous(), weight_scale.contiguous())
+    sb = _weight_scales_f32(weight, weight_scale)
+    xq, xs = _act_quant_stepmajor(x, round_scale)
+    return _fp8_gemm_raw(xq, xs, 1, weight.contiguous(), sb.contiguous())

@@ -91,11 +91,20 @@ def _per_row_quant(x2d: Tensor, eps: float) -> tuple[Tensor, Tensor]:
 
 def quantize_weight_fp8_per_channel(weight: Tensor) -> tuple[Tensor, Tensor]:
     """Quantize an [N, K] weight with one FP8 scale per output channel (fp8.py:129-138):
-    ``s[n] = max(amax_k |W[n,k]| / 448, 1e-10)``; returns ``(wq [N,K], s [1,N])``."""
+    ``s[n] = max(amax_k |W[n,k]| / 448, 1e-10)`` with the division done as torch does
+    it on a GPU tensor (a multiply by fl32(1/448)); returns ``(wq [N,K], s [1,N])``."""
     if weight.ndim != 2:
         raise ValueError("FP8 linear weights must have shape [N, K]")
-    wq, s = _per_row_quant(weight, 1e-10)
-    return wq, s.transpose(0, 1).contiguous()
+    _lib.require_device(weight)
+    if weight.dtype not in _ACT_DTYPES:
+        raise ValueError("FP8 quantization input must be bf16 or fp16")
+    w = weight.contiguous()
+    n, k = w.shape
+    wq = torch.empty((n, k), dtype=FP8_E4M3, device=w.device)
+    ws = torch.empty((1, n), dtype=torch.float32, device=w.device)
+    _lib.call("ti_fp8_quant_weight_per_channel", w.data_ptr(), _lib.dtype_code(w.dtype), n, k,
+              wq.data_ptr(), ws.data_ptr(), _lib.stream_of(w))
+    return wq, ws
 
 
 def quantize_activation_fp8_per_token(x: Tensor) -> tuple[Tensor, Tensor]:

@@ -157,8 +157,14 @@ def _workspace(device: torch.device, nbytes: int) -> Tensor:
         return ws
 
 
+def _round_scale(scale_fmt: str | None) -> int:
+    """act_quant's ``scale_fmt`` (deepseek_v4_tilelang_definitions.py:255-331): any
+    format rounds the 1x128 activation scales up to powers of two."""
+    return int(scale_fmt is not None)
+
+
 def _routed(entry: str, hidden_states: Tensor, topk_weights: Tensor, topk_ids: Tensor, experts,
-            clamp_limit: float) -> Tensor:
+            clamp_limit: float, scale_fmt: str | None) -> Tensor:
     if hidden_states.ndim != 2 or not hidden_states.is_contiguous():
         raise ValueError("hidden_states must be a contiguous matrix")
     if hidden_states.dtype != torch.bfloat16:
@@ -184,29 +190,35 @@ def _routed(entry: str, hidden_states: Tensor, topk_weights: Tensor, topk_ids: T
     layout = (1,) if entry == "ti_fp4_moe" else ()  # MXFP4 scales are prepared step-major
     _lib.call(entry, hidden_states.data_ptr(), weights.data_ptr(), local_ids.data_ptr(), tokens, k,
               experts.w13.data_ptr(), experts.w13_scale.data_ptr(), experts.w2.data_ptr(),
-              experts.w2_scale.data_ptr(), *layout, e_local, hidden, inter, float(clamp_limit), out.data_ptr(),
+              experts.w2_scale.data_ptr(), *layout, e_local, hidden, inter, float(clamp_limit),
+              _round_scale(scale_fmt), out.data_ptr(),
               aligned, ws.numel() - (aligned - base), _lib.stream_of(hidden_states))
     return out
 
 
 def fused_fp8_moe(hidden_states: Tensor, topk_weights: Tensor, topk_ids: Tensor,
-                  experts: PreparedFp8Experts, *, clamp_limit: float = 0.0) -> Tensor:
+                  experts: PreparedFp8Experts, *, clamp_limit: float = 0.0,
+                  scale_fmt: str | None = None) -> Tensor:
     """Grouped routed experts for one GPU (signature of fused_mxfp4_moe,
     deepseek_v4_marlin.py:311-318).  ``topk_ids`` are global expert ids; routes to
-    experts this GPU does not hold contribute nothing.  Returns bf16 [T, H]."""
-    return _routed("ti_fp8_moe", hidden_states, topk_weights, topk_ids, experts, clamp_limit)
+    experts this GPU does not hold contribute nothing.  ``scale_fmt`` is the
+    model's act_quant scale format (DSv4 sets "ue8m0": power-of-two activation
+    scales, tensor_parallel.py:195-207,1199-1211).  Returns bf16 [T, H]."""
+    return _routed("ti_fp8_moe", hidden_states, topk_weights, topk_ids, experts, clamp_limit, scale_fmt)
 
 
 def fused_mxfp4_moe(hidden_states: Tensor, topk_weights: Tensor, topk_ids: Tensor,
-                    experts: PreparedMxfp4Experts, *, clamp_limit: float = 0.0) -> Tensor:
+                    experts: PreparedMxfp4Experts, *, clamp_limit: float = 0.0,
+                    scale_fmt: str | None = None) -> Tensor:
     """MXFP4 routed experts (deepseek_v4_marlin.py:311-411, same arguments and
-    [T, H] bf16 result); see ``fused_fp8_moe`` for routing semantics."""
-    return _routed("ti_fp4_moe", hidden_states, topk_weights, topk_ids, experts, clamp_limit)
+    [T, H] bf16 result); see ``fused_fp8_moe`` for routing and ``scale_fmt``."""
+    return _routed("ti_fp4_moe", hidden_states, topk_weights, topk_ids, experts, clamp_limit, scale_fmt)
 
 
 def moe_forward(hidden_states: Tensor, router_logits: Tensor, experts: PreparedFp8Experts, k: int, *,
-                renormalize: bool = True, route_scale: float = 1.0, clamp_limit: float = 0.0) -> Tensor:
+                renormalize: bool = True, route_scale: float = 1.0, clamp_limit: float = 0.0,
+                scale_fmt: str | None = None) -> Tensor:
     """Router + routed experts: the routed part of DSv4 MoE.forward (without the
     shared expert and the cross-GPU all-reduce)."""
     w, ids = route_topk(router_logits, k, renormalize=renormalize, route_scale=route_scale)
-    return fused_fp8_moe(hidden_states, w, ids, experts, clamp_limit=clamp_limit)
+    return fused_fp8_moe(hidden_states, w, ids, experts, clamp_limit=clamp_limit, scale_fmt=scale_fmt)

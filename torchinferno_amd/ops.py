@@ -18,7 +18,8 @@ Ops (each a thin wrapper over ``torchinferno_amd.kernels.*`` and libti_quant.so)
   (deepseek_v4_tilelang.py:147-223);
 * ``moe_route_topk(logits, k, renormalize, route_scale) -> (Tensor, Tensor)`` and
   ``fused_fp8_moe(hidden, topk_weights, topk_ids, w13, w13_scale, w2, w2_scale,
-  clamp_limit) -> Tensor`` -- the routed-expert slot (deepseek_v4_marlin.py:311);
+  clamp_limit, round_scale=False) -> Tensor`` -- the routed-expert slot
+  (deepseek_v4_marlin.py:311); ``round_scale`` is act_quant's ue8m0 scale format;
 * ``rms_norm_fp8_per_token(x, weight, eps) -> (q, scale)``,
   ``add_rms_norm_fp8_per_token(x, residual, weight, eps) -> (hidden, q, scale)``,
   ``swiglu_fp8_per_token(gate, up) -> (q, scale)`` -- the fused producers of the
@@ -124,17 +125,19 @@ def _moe_route_topk_fake(logits, k, renormalize, route_scale):
 
 @torch.library.custom_op(f"{_NS}::fused_fp8_moe", mutates_args=())
 def fused_fp8_moe(hidden: Tensor, topk_weights: Tensor, topk_ids: Tensor, w13: Tensor, w13_scale: Tensor,
-                  w2: Tensor, w2_scale: Tensor, clamp_limit: float) -> Tensor:
+                  w2: Tensor, w2_scale: Tensor, clamp_limit: float, round_scale: bool = False) -> Tensor:
     e, two_i, h = w13.shape
     experts = moe.PreparedFp8Experts(
         w13=w13, w13_scale=w13_scale, w2=w2, w2_scale=w2_scale,
         expert_map=torch.arange(e, dtype=torch.int32, device=w13.device),
         global_num_experts=e, hidden_size=h, intermediate_size=two_i // 2)
-    return moe.fused_fp8_moe(hidden, topk_weights, topk_ids, experts, clamp_limit=clamp_limit)
+    return moe.fused_fp8_moe(hidden, topk_weights, topk_ids, experts, clamp_limit=clamp_limit,
+                             scale_fmt="ue8m0" if round_scale else None)
 
 
 @fused_fp8_moe.register_fake
-def _fused_fp8_moe_fake(hidden, topk_weights, topk_ids, w13, w13_scale, w2, w2_scale, clamp_limit):
+def _fused_fp8_moe_fake(hidden, topk_weights, topk_ids, w13, w13_scale, w2, w2_scale, clamp_limit,
+                        round_scale=False):
     return torch.empty_like(hidden)
 
 
