@@ -101,6 +101,19 @@ int ti_w4a16_gemm(const void* a, int dtype, const int32_t* packed_weight,
                   const void* packed_scales, void* out, int M, int N, int K, int group_size,
                   void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Allocation-free ti_w4a16_gemm (no counterpart in the reference): for callers
+ * that cannot allocate device memory -- code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  Same arguments and results
+ * as ti_w4a16_gemm without the workspace: split-K partials and tickets live in
+ * a static per-GPU device buffer of ti_w4a16_noalloc_scratch_bytes() (16 MiB),
+ * set up on the first call on each device.  Problems needing more split-K
+ * scratch than that return TI_ERR_WORKSPACE.  All calls on one GPU share the
+ * buffer: calls that overlap on one GPU (unordered streams or threads) race. */
+int ti_w4a16_gemm_noalloc(const void* a, int dtype, const int32_t* packed_weight,
+                          const void* packed_scales, void* out, int M, int N, int K,
+                          int group_size, hipStream_t stream);
+size_t ti_w4a16_noalloc_scratch_bytes(void);
+
 /* ---------------------------------------------------------------------------
  * FP8 e4m3 (OCP float8_e4m3fn) quantizers.  fp32 arithmetic with IEEE
  * division, round-to-nearest-even cast: codes and scales are bit-identical to
