@@ -5,8 +5,10 @@ Headline workload: the int4 W4A16 group-128 decode
 sweep at Llama-3-8B MLP shapes -- gate_up (K=4096, N=28672) and down (K=14336,
 N=4096), M in {1, 8, 32, 128}, bf16 activations ~ N(0,1), codes ~ U{0..15}, zero
 point 8, bf16 scales ~ U[0.002, 0.02].  One *step* is one pass over the sweep:
-the 8 GEMMs, each on the next of a rotating set of weight copies (>= 512 MiB per
-shape, twice the 256 MiB Infinity Cache) so bytes come from HBM.  ``value`` is
+the 8 GEMMs, each on the next copy of its shape from a rotating set shared by
+all M points of that shape (>= 512 MiB per shape, twice the 256 MiB Infinity
+Cache), so no launch re-reads a copy another launch has just brought on chip and
+bytes come from HBM.  ``value`` is
 HBM GB/s over the packed-weight + scale bytes of a step (the config's unit).
 
 ``roofline`` describes the launch that dominates a step's time, with its
@@ -16,8 +18,9 @@ config measured the same way: config 0 (int4 fp16), config 2 (FP8 per-token x
 per-channel, Llama-3-70B, plus its fused add+RMSNorm / SwiGLU -> FP8
 activation producers), config 3 (DeepSeek 128x128 block FP8, and the same
 shapes with MXFP4 weights) and config 4 (routed FP8 MoE, 256 experts, top-8,
-router included, and the same experts in MXFP4).  ``cpu_baseline`` times
-the CPU oracle (dequantize-then-matmul, oracle/int4.py) on one gate_up M=32 GEMM.
+router included, and the same experts in MXFP4).  ``cpu_baseline`` times the
+reference's PyTorch CPU path (dequantize, then an fp32 matmul) on one config-1
+gate_up M=32 GEMM; ``cpu_points`` does the same for samples of configs 2, 3 and 4.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only int4|fp8|moe]
 """
@@ -54,40 +57,132 @@ def weight_bytes(k, n):
     return k * n // 2 + (k // 128) * n * 2
 
 
-def cpu_baseline(seconds_budget: float = 20.0) -> dict:
-    """Time the CPU oracle on one gate_up M=32 GEMM (bounded sample)."""
-    import numpy as np
-    from oracle import int4 as oint4
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        threads = 1
-    k, n = SHAPES["gate_up"]
-    m = 32
-    rng = np.random.default_rng(0)
-    codes = rng.integers(0, 16, (k, n), dtype=np.uint8)
-    q = oint4.pack_int4(codes)
-    s = rng.uniform(0.002, 0.02, (k // 128, n)).astype(np.float32)
-    a = rng.standard_normal((m, k)).astype(np.float32)
+def _cpu_time(fn, budget_s):
+    """Median seconds of fn() over up to 3 runs after one warm-up, stopping early
+    once `budget_s` is spent; returns (median, runs)."""
+    fn()
     times = []
     t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < 1.0):
+    while len(times) < 3:
         t0 = time.perf_counter()
-        oint4.w4a16_reference(a, q, s)
+        fn()
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > seconds_budget:
+        if time.perf_counter() - t_start > budget_s:
             break
-    med = statistics.median(times)
-    return {
-        "value": round(weight_bytes(k, n) / med / 1e9, 3),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"one gate_up GEMM (M=32, K=4096, N=28672): unpack + (q-8)*s + fp32 "
-                   f"matmul (oracle/int4.py w4a16_reference), median of {len(times)} runs, "
-                   f"{med * 1e3:.1f} ms each; host has {os.cpu_count()} logical CPUs"),
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(budget_s: float = 6.0) -> tuple[dict, list]:
+    """The reference's PyTorch CPU path on the box's host cores, on bounded samples
+    of the BASELINE workloads (dequantize, then an fp32 matmul):
+
+    * int4 (config 1, gate_up M=32): unpack the int32 words, ``(q - 8) * s`` in fp32,
+      ``a.float() @ w`` -- ``_dequant_ref``, tests/test_marlin_int4.py:40-49;
+    * FP8 per-token x per-channel (config 2, qkv M=64): ``xq.float() * xs`` and
+      ``wq.float() * ws``, fp32 matmul;
+    * block FP8 (config 3 a, M=16): ``dequantize_block_fp8``
+      (src/torchinferno/models/deepseek_v4/ops.py:180-188) + matmul;
+    * MoE (config 4 T=64): the per-expert loop of MoE.forward
+      (src/torchinferno/models/deepseek_v4/tensor_parallel.py:899-907) over 8 of
+      the touched experts, scaled to all of them.
+
+    Threads: torch.get_num_threads(), i.e. OMP_NUM_THREADS where set (the box's CPU
+    share), else torch's default.  Returns (the int4 record, the other records)."""
+    import torch
+    threads = torch.get_num_threads()
+    host = f"{threads} threads (torch.get_num_threads) of {os.cpu_count()} logical CPUs"
+    g = torch.Generator().manual_seed(0)
+
+    def e4m3(*shape):
+        return torch.randint(-120, 120, shape, generator=g, dtype=torch.int8).view(torch.float8_e4m3fn)
+
+    # int4 gate_up M=32
+    k, n = SHAPES["gate_up"]
+    m = 32
+    words = torch.randint(-2**31, 2**31 - 1, (k // 8, n), generator=g, dtype=torch.int32)
+    sc = torch.rand((k // 128, n), generator=g) * 0.018 + 0.002
+    a = torch.randn((m, k), generator=g)
+    shifts = torch.arange(0, 32, 4, dtype=torch.int32).view(1, 8, 1)
+
+    def deq4():
+        q = ((words.view(k // 8, 1, n) >> shifts) & 0xF).view(k, n)
+        return (q.float() - 8.0) * sc.repeat_interleave(128, 0)
+
+    w = deq4()
+    t_deq, r1 = _cpu_time(deq4, budget_s)
+    t_mm, r2 = _cpu_time(lambda: a @ w, budget_s)
+    t = t_deq + t_mm
+    int4 = {
+        "value": round(weight_bytes(k, n) / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": (f"one config-1 gate_up GEMM (M=32, K=4096, N=28672) on torch CPU: unpack + (q-8)*s "
+                   f"{t_deq * 1e3:.1f} ms + fp32 matmul {t_mm * 1e3:.1f} ms (medians of {r1}/{r2} runs); {host}"),
     }
+    del w, words
+    recs = []
+
+    # FP8 rowcol: config 2 qkv M=64
+    k, n, m = 8192, 10240, 64
+    wq, ws = e4m3(n, k), torch.rand((1, n), generator=g) * 1e-3
+    xq, xs = e4m3(m, k), torch.rand((m, 1), generator=g) * 1e-2
+    t_deq, _ = _cpu_time(lambda: wq.float() * ws.t(), budget_s)
+    wd = wq.float() * ws.t()
+    t_mm, runs = _cpu_time(lambda: (xq.float() * xs) @ wd.t(), budget_s)
+    t = t_deq + t_mm
+    recs.append({"point": "cpu config2 fp8 rowcol qkv M=64 K=8192 N=10240", "us": round(t * 1e6, 1),
+                 "TFLOPs": round(2 * m * n * k / t / 1e12, 4), "algo_GBs": round((n * k + m * k) / t / 1e9, 3),
+                 "dequant_ms": round(t_deq * 1e3, 2), "matmul_ms": round(t_mm * 1e3, 2), "cores": threads,
+                 "kind": "port"})
+    del wq, wd
+
+    # block FP8: config 3 a M=16
+    k, n, m = 7168, 18432, 16
+    bq, bs = e4m3(n, k), torch.rand((n // 128, k // 128), generator=g) * 1e-3
+    aq, a_s = e4m3(m, k), torch.rand((m, k // 128), generator=g) * 1e-2
+
+    def deq_block(w, s):
+        full = s.repeat_interleave(128, 0).repeat_interleave(128, 1)[: w.size(0), : w.size(1)]
+        return w.float() * full
+
+    t_deq, _ = _cpu_time(lambda: deq_block(bq, bs), budget_s)
+    bd = deq_block(bq, bs)
+    t_mm, _ = _cpu_time(lambda: (aq.float() * a_s.repeat_interleave(128, 1)) @ bd.t(), budget_s)
+    t = t_deq + t_mm
+    recs.append({"point": "cpu config3 fp8 block a M=16 K=7168 N=18432", "us": round(t * 1e6, 1),
+                 "TFLOPs": round(2 * m * n * k / t / 1e12, 4), "algo_GBs": round((n * k + m * k) / t / 1e9, 3),
+                 "dequant_ms": round(t_deq * 1e3, 2), "matmul_ms": round(t_mm * 1e3, 2), "cores": threads,
+                 "kind": "port"})
+    del bq, bd
+
+    # MoE: config 4 T=64, per-expert loop over a sample of experts
+    e_tot, h, inter, topk, tok = 256, 7168, 2048, 8, 64
+    logits = torch.randn((tok, e_tot), generator=g)
+    ids = torch.topk(torch.softmax(logits, -1), topk, dim=-1).indices
+    touched = torch.unique(ids)
+    x = torch.randn((tok, h), generator=g).to(torch.bfloat16)
+    sample = touched[:8].tolist()
+    experts = {ei: (e4m3(2 * inter, h), torch.rand((2 * inter // 128, h // 128), generator=g) * 1e-3,
+                    e4m3(h, inter), torch.rand((h // 128, inter // 128), generator=g) * 1e-3) for ei in sample}
+
+    def moe_loop():
+        y = torch.zeros((tok, h))
+        for ei in sample:
+            w13, s13, w2, s2 = experts[ei]
+            rows, slot = torch.where(ids == ei)
+            xe = x[rows].float()
+            gu = xe @ deq_block(w13, s13).t()
+            act = torch.nn.functional.silu(gu[:, :inter]) * gu[:, inter:]
+            y[rows] += act.to(torch.bfloat16).float() @ deq_block(w2, s2).t()
+        return y
+
+    t_s, runs = _cpu_time(moe_loop, budget_s)
+    t = t_s * touched.numel() / len(sample)
+    recs.append({"point": f"cpu config4 fp8 moe T={tok} experts_touched={touched.numel()}",
+                 "us": round(t * 1e6, 1), "tokens_per_s": round(tok / t, 2),
+                 "algo_GBs": round(touched.numel() * (3 * inter * h) / t / 1e9, 3), "cores": threads,
+                 "kind": "port",
+                 "sample": f"{len(sample)} of the {touched.numel()} touched experts, median of {runs} runs, "
+                           f"scaled by {touched.numel()}/{len(sample)}"})
+    return int4, recs
 
 
 def timed_burst(launch_fns, reps, stream_handle):
@@ -116,6 +211,21 @@ def _check(name, st):
 # --------------------------------------------------------------------------- int4
 
 
+class Rotation:
+    """Weight copies of one shape, handed out in turn to every launch of that shape,
+    so consecutive launches -- of any M -- read different copies and a copy comes
+    back only after >= ROTATE_BYTES of other weights have streamed past it."""
+
+    def __init__(self, copies):
+        self.copies = copies
+        self.i = 0
+
+    def next(self):
+        c = self.copies[self.i % len(self.copies)]
+        self.i += 1
+        return c
+
+
 class Int4Point:
     def __init__(self, name, k, n, m, dev, copies, dtype_code=2):
         import torch
@@ -126,15 +236,13 @@ class Int4Point:
         self.dtype_code = dtype_code
         self.a = torch.randn((m, k), device=dev, dtype=dt)
         self.out = torch.empty((m, n), device=dev, dtype=dt)
-        self.copies = copies
+        self.copies = copies if isinstance(copies, Rotation) else Rotation(copies)
         self.ws = ti4.make_workspace(n, dev, size_k=k, max_m=m)
         self.fn = _lib.lib().ti_w4a16_gemm
         self.ws_bytes = self.ws.numel() * 4
-        self.i = 0
 
     def launch(self, stream):
-        pw, ps = self.copies[self.i % len(self.copies)]
-        self.i += 1
+        pw, ps = self.copies.next()
         _check("ti_w4a16_gemm", self.fn(self.a.data_ptr(), self.dtype_code, pw.data_ptr(), ps.data_ptr(),
                                         self.out.data_ptr(), self.m, self.n, self.k, 128, self.ws.data_ptr(),
                                         self.ws_bytes, stream))
@@ -207,7 +315,8 @@ def point_record(label, t_s, algo_bytes, flops, bound, peak_tf, extra=None):
 
 
 def fp8_points(dev, stream):
-    """Config 2 (rowcol) and config 3 (block) GEMMs, excluding activation quant."""
+    """Config 2 (rowcol) and config 3 (block) GEMMs on pre-quantized activations, and
+    config 2 at M=64 and 4096 again with the per-token activation quant timed in."""
     import torch
     from torchinferno_amd import _lib
     L = _lib.lib()
@@ -260,9 +369,59 @@ def fp8_points(dev, stream):
                 recs.append(point_record(f"{label} {sname} M={m} K={k} N={n}", t, algo, flops, bound,
                                          FP8_PEAK_TFLOPS))
                 log(recs[-1])
+                if mode == 0 and m in (64, 4096):
+                    # config 2 as specified: bf16 activations quantized per token inside the
+                    # timed region (quant kernel + GEMM), the reference's "incl. dynamic quant"
+                    # figure (scripts/bench_fp8_prefill.py:13-17)
+                    x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+
+                    def launch_q(st, x=x, a=a, asc=asc, m=m, k=k, launch=launch):
+                        _check("fp8 quant", L.ti_fp8_quant_per_token(x.data_ptr(), 2, m, k, 1e-10, a.data_ptr(),
+                                                                     asc.data_ptr(), st))
+                        launch(st)
+
+                    timed_burst([launch_q], 3, stream)
+                    t = timed_burst([launch_q], reps, stream) / reps * 1e-3
+                    algo_q = algo + m * k * 2 + m * k + m * 4  # + x read, codes and scales written
+                    bound_q = "mfma" if flops / algo_q > FP8_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
+                    recs.append(point_record(f"{label} incl. per-token quant {sname} M={m} K={k} N={n}", t,
+                                             algo_q, flops, bound_q, FP8_PEAK_TFLOPS))
+                    log(recs[-1])
+                    del x
             del bq, bs
             torch.cuda.empty_cache()
     return recs
+
+
+def fp8_single_point(spec, launches, dev, stream):
+    """Launch one config-2 (``rowcol:SHAPE:M``) or config-3 (``block:SHAPE:M``) GEMM
+    `launches` times over rotating weight copies: the program a counter run profiles."""
+    import torch
+    from torchinferno_amd import _lib
+    L = _lib.lib()
+    mode_name, sname, m = spec.split(":")
+    m = int(m)
+    mode = {"rowcol": 0, "block": 1}[mode_name]
+    k, n = (FP8_SHAPES if mode == 0 else BLOCK_SHAPES)[sname]
+    ncopy = max(2, -(-ROTATE_BYTES // (n * k)))
+    bq = [torch.randint(-120, 120, (n, k), device=dev, dtype=torch.int8) for _ in range(ncopy)]
+    bs = [torch.rand((n,) if mode == 0 else (-(-n // 128), k // 128), device=dev) * 1e-3 + 1e-4
+          for _ in range(ncopy)]
+    a = torch.randint(-120, 120, (m, k), device=dev, dtype=torch.int8)
+    asc = torch.rand((m,) if mode == 0 else (k // 128, m), device=dev) * 0.01 + 1e-3
+    out = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
+    ws = torch.zeros(64 << 20, dtype=torch.int32, device=dev)
+    for i in range(launches):
+        j = i % ncopy
+        if mode == 0:
+            r = L.ti_fp8_gemm_rowcol(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(), 1,
+                                     out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, stream)
+        else:
+            r = L.ti_fp8_gemm_block(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(),
+                                    out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, stream)
+        _check("fp8 gemm", r)
+    torch.cuda.synchronize()
+    print(json.dumps({"point": spec, "launches": launches}), flush=True)
 
 
 # --------------------------------------------------------------------------- fused producers
@@ -390,7 +549,8 @@ def main():
     ap.add_argument("--only", choices=["int4", "fp8", "moe"], default=None,
                     help="run only one family of points (profiling)")
     ap.add_argument("--point", default=None,
-                    help="NAME:M -- launch only that config-1 int4 point, --steps times (counter runs)")
+                    help="NAME:M -- launch only that config-1 int4 point, --steps times (counter runs); "
+                         "rowcol:SHAPE:M / block:SHAPE:M for a config-2 / config-3 FP8 GEMM")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -409,6 +569,9 @@ def main():
     log(f"device: {props.name} CUs={props.multi_processor_count}")
     stream = torch.cuda.current_stream(dev).cuda_stream
 
+    if args.point and args.point.count(":") == 2:
+        fp8_single_point(args.point, args.steps, dev, stream)
+        return
     if args.point:
         name, m = args.point.split(":")
         k, n = SHAPES[name]
@@ -440,8 +603,8 @@ def main():
 
     points = []
     for name, (k, n) in SHAPES.items():
-        copies = make_int4_copies(k, n, dev)
-        log(f"{name}: K={k} N={n} copies={len(copies)}")
+        copies = Rotation(make_int4_copies(k, n, dev))
+        log(f"{name}: K={k} N={n} copies={len(copies.copies)}")
         for m in MS:
             points.append(Int4Point(name, k, n, m, dev, copies))
 
@@ -496,10 +659,10 @@ def main():
         "algo_bytes_per_launch": dom.algo_bytes, "flops_per_launch": dom.flops,
         "share_of_step": round(t_dom * 1e3 / ms_per_step, 3),
     }
-    cpu = None
+    cpu, cpu_points = None, []
     if not args.no_cpu_baseline:
         log("timing CPU baseline ...")
-        cpu = cpu_baseline()
+        cpu, cpu_points = cpu_baseline()
     line = {
         "metric": "TFLOP/s and HBM GB/s vs roofline, int4/FP8 GEMM at Llama-3 8B/70B shapes",
         "value": round(value, 1),
@@ -519,6 +682,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "points": pts + extra_points,
+        "cpu_points": cpu_points,
         "wall_s": round(wall, 3),
     }
     print(json.dumps(line), flush=True)
