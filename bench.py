@@ -550,7 +550,8 @@ def main():
                     help="run only one family of points (profiling)")
     ap.add_argument("--point", default=None,
                     help="NAME:M -- launch only that config-1 int4 point, --steps times (counter runs); "
-                         "rowcol:SHAPE:M / block:SHAPE:M for a config-2 / config-3 FP8 GEMM")
+                         "rowcol:SHAPE:M / block:SHAPE:M for a config-2 / config-3 FP8 GEMM; "
+                         "'copy' for a 256 MiB copy (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -569,6 +570,15 @@ def main():
     log(f"device: {props.name} CUs={props.multi_processor_count}")
     stream = torch.cuda.current_stream(dev).cuda_stream
 
+    if args.point == "copy":
+        # counter calibration: a plain 256 MiB device-to-device copy (torch's copy kernel)
+        src = torch.ones((64 << 20,), dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"point": "copy", "bytes_read": src.numel() * 4, "launches": args.steps}), flush=True)
+        return
     if args.point and args.point.count(":") == 2:
         fp8_single_point(args.point, args.steps, dev, stream)
         return

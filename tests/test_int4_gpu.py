@@ -236,3 +236,32 @@ def test_decode_kernel_sixteen_waves(dev, monkeypatch, plan, m, n):
     out, ref = _run_gemm(dev, m, 2048, n, torch.float16 if m % 2 else torch.bfloat16, 80 + m)
     assert _rel_err(out.float().cpu().numpy(), ref) <= TOL
 
+
+
+# (nt:waves:depth:splits, M) for every instantiated streaming-kernel configuration
+# (int4_stream.hip), forced through TI_ROCM_W4A16_STREAM on a small problem: ragged
+# M inside the row tile, K ranges that do not divide evenly over the waves, and
+# the split-K ticket reduction.
+_STREAM_CASES = [("7:8:2:1", 5), ("7:8:2:1", 29), ("7:16:1:1", 11), ("2:8:4:2", 8), ("4:8:2:4", 13),
+                 ("4:16:1:4", 27), ("1:8:4:1", 3), ("1:16:2:1", 1), ("2:16:1:2", 20), ("2:8:4:3", 1)]
+
+
+@pytest.mark.parametrize("plan,m", _STREAM_CASES)
+def test_stream_kernel_configs(dev, monkeypatch, plan, m):
+    import ctypes
+    from torchinferno_amd import _lib
+    from torchinferno_amd.kernels import int4 as ti4
+    nt = int(plan.split(":")[0])
+    k, n = 128 * 19, 16 * nt * 8
+    monkeypatch.setenv("TI_ROCM_W4A16_STREAM", plan)
+    buf = ctypes.create_string_buffer(256)
+    _lib.lib().ti_w4a16_plan_name(m, n, k, 128, buf, 256)
+    print(f"[int4] stream {plan} M={m}: {buf.value.decode()}", flush=True)
+    assert buf.value.startswith(b"w4a16_stream_kernel"), buf.value
+    a, qweight, scales, pw, ps, ws = _setup(m, k, n, torch.bfloat16, m + nt, dev)
+    out = ti4.int4_mm(a.to(dev), pw, ps, ws, n, k)
+    out2 = ti4.int4_mm(a.to(dev), pw, ps, ws, n, k)
+    torch.cuda.synchronize()
+    ref = oint4.w4a16_reference(to_np32(a), qweight.numpy(), to_np32(scales))
+    assert _rel_err(out.float().cpu().numpy(), ref) <= TOL
+    assert torch.equal(out, out2)  # deterministic, tickets left at zero

@@ -35,6 +35,7 @@
 // split partials are summed in split order by the last workgroup of the tile
 // (or by a second kernel), so results are deterministic and nothing is memset.
 #include "int4_decode.h"
+#include "int4_stream.h"
 
 namespace ti {
 namespace int4 {
@@ -555,6 +556,11 @@ struct WsNeed {
 };
 
 static WsNeed ws_need(int M, int N, int K) {
+  StreamPlan sp;
+  if (make_stream_plan(M, N, K, sp)) {
+    if (sp.splits <= 1) return {0, 0};
+    return {stream_partial_bytes(sp, M, N), stream_ticket_bytes(sp)};
+  }
   if (use_decode(M, K)) {
     DecodePlan d = make_decode_plan(M, N, K);
     if (d.splits <= 1) return {0, 0};
@@ -569,7 +575,11 @@ extern "C" int ti_w4a16_plan_name(int M, int N, int K, int group_size, char* buf
   TI_CHECK_ARG(buf && len > 0, "ti_w4a16_plan_name: null buffer");
   TI_CHECK_SHAPE(group_size == kGroup && M >= 1 && N > 0 && K > 0 && K % kGroup == 0 && N % 64 == 0,
                  "ti_w4a16_plan_name: need M >= 1, K %% 128 == 0, N %% 64 == 0");
-  if (use_decode(M, K)) {
+  StreamPlan sp;
+  if (make_stream_plan(M, N, K, sp)) {
+    snprintf(buf, len, "w4a16_stream_kernel mt=%d nt=%d waves=%d depth=%d splits=%d lds=%d", sp.mt, sp.nt,
+             sp.waves, sp.depth, sp.splits, sp.lds);
+  } else if (use_decode(M, K)) {
     DecodePlan d = make_decode_plan(M, N, K);
     snprintf(buf, len, "w4a16_decode_kernel mr=%d nt=%d wk=%d waves=%d ring=%d splits=%d mchunks=%d lds=%d", d.mr,
              d.nt, d.wk, d.waves, d.ring, d.splits, d.mchunks, d.lds);
@@ -680,6 +690,25 @@ extern "C" int ti_w4a16_gemm(const void* a, int dtype, const int32_t* packed_wei
                ((uintptr_t)packed_scales & 15) == 0,
                "ti_w4a16_gemm: a, packed_weight and packed_scales must be 16-byte aligned");
   TI_CHECK_ARG(((uintptr_t)out & 7) == 0, "ti_w4a16_gemm: out must be 8-byte aligned");
+  StreamPlan sp;
+  if (make_stream_plan(M, N, K, sp)) {
+    StreamArgs x{(const uint16_t*)a, (const i32x4*)packed_weight, (const uint16_t*)packed_scales,
+                 (uint16_t*)out, nullptr, nullptr, M, N, K};
+    if (sp.splits > 1) {
+      const size_t need = stream_partial_bytes(sp, M, N) + stream_ticket_bytes(sp) + 256;
+      if (!workspace || workspace_bytes_ < need) {
+        set_error("ti_w4a16_gemm: workspace of %zu bytes required (got %zu)", need, workspace_bytes_);
+        return TI_ERR_WORKSPACE;
+      }
+      TI_CHECK_ARG(((uintptr_t)workspace & 15) == 0, "ti_w4a16_gemm: workspace must be 16-byte aligned");
+      x.partial = (float*)workspace;
+      const uintptr_t end = ((uintptr_t)workspace + workspace_bytes_) & ~(uintptr_t)255;
+      x.tickets = (int*)(end - stream_ticket_bytes(sp));
+    }
+    launch_stream(sp, dtype, x, stream);
+    TI_CHECK_LAUNCH("ti_w4a16_gemm");
+    return TI_OK;
+  }
   if (use_decode(M, K)) {
     DecodePlan d = make_decode_plan(M, N, K);
     TI_CHECK_SHAPE(d.lds <= kDecodeLdsMax, "ti_w4a16_gemm: decode plan needs %d bytes of LDS", d.lds);
