@@ -48,7 +48,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .numerics import E4M3_MAX, e4m3_decode, e4m3_encode, round_to
+from .numerics import E4M3_MAX, e4m3_decode, e4m3_decode64, e4m3_encode, round_to
 
 F32 = np.float32
 _INV_MAX = F32(1.0) / F32(E4M3_MAX)  # 1/448 rounded to fp32, the TileLang constant
@@ -160,8 +160,8 @@ def fp8_gemm_block(a_codes: np.ndarray, a_s: np.ndarray, b_codes: np.ndarray,
                    b_s: np.ndarray, block: int = 128) -> np.ndarray:
     """Per-K-block partial sums scaled by a_s[m,j]*b_s[n//128,j], accumulated in
     fp32 (deepseek_v4_tilelang_definitions.py:470-483).  Returns fp32 [M,N]."""
-    a = e4m3_decode(a_codes).astype(np.float64)
-    b = e4m3_decode(b_codes).astype(np.float64)
+    a = e4m3_decode64(a_codes)
+    b = e4m3_decode64(b_codes)
     m, k = a.shape
     n = b.shape[0]
     kb = -(-k // block)

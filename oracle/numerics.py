@@ -41,8 +41,16 @@ def e4m3_decode_table() -> np.ndarray:
 _E4M3_TABLE = e4m3_decode_table()
 
 
+_E4M3_TABLE64 = _E4M3_TABLE.astype(np.float64)
+
+
 def e4m3_decode(codes: np.ndarray) -> np.ndarray:
     return _E4M3_TABLE[np.asarray(codes, dtype=np.uint8)]
+
+
+def e4m3_decode64(codes: np.ndarray) -> np.ndarray:
+    """e4m3 codes -> exact values as fp64 (one table lookup)."""
+    return _E4M3_TABLE64[np.asarray(codes, dtype=np.uint8)]
 
 
 def e4m3_encode(x: np.ndarray) -> np.ndarray:
