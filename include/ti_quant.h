@@ -101,6 +101,15 @@ int ti_w4a16_gemm(const void* a, int dtype, const int32_t* packed_weight,
                   const void* packed_scales, void* out, int M, int N, int K, int group_size,
                   void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Asymmetric zero points (GPTQ / AWQ checkpoints; the reference has only the
+ * symmetric lazy RTN of src/torchinferno/kernels/marlin.py:108-131 that they
+ * replace): with W = (q - z) * s, after ti_w4a16_gemm computed the symmetric
+ * part (q - 8) * s into out, adds sum_g rowsum_g(a[m]) * zero_offset[g, n] where
+ * zero_offset = (8 - z) * s (fp32 [K/128, N]), in fp32, and rounds to dtype.
+ * a [M, K] and out [M, N] in dtype; N % 4 == 0, K % 128 == 0. */
+int ti_w4a16_zero_point_add(const void* a, int dtype, const float* zero_offset, void* out,
+                            int M, int N, int K, hipStream_t stream);
+
 /* Allocation-free ti_w4a16_gemm (no counterpart in the reference): for callers
  * that cannot allocate device memory -- code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc.  Same arguments and results

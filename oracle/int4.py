@@ -66,6 +66,21 @@ def dequant_int4(qweight: np.ndarray, scales: np.ndarray, group_size: int = 128)
     return codes.astype(np.float32) * s_full
 
 
+def dequant_int4_zp(qweight: np.ndarray, scales: np.ndarray, zeros: np.ndarray,
+                    group_size: int = 128) -> np.ndarray:
+    """Asymmetric group-wise int4 (GPTQ / AWQ checkpoints): (q - z) * s as fp32 [K, N],
+    z the per-(group, column) zero point in [0, 15] -- the published GPTQ / AWQ
+    dequantization (AWQ stores z, GPTQ "v1" stores z - 1; the caller passes z).
+    Exact in fp32 for the same reason as ``dequant_int4``."""
+    codes = unpack_int4(qweight).astype(np.int32)
+    s = np.asarray(scales, dtype=np.float32)
+    z = np.asarray(zeros, dtype=np.int32)
+    k, n = codes.shape
+    if s.shape != (k // group_size, n) or z.shape != s.shape:
+        raise ValueError(f"scales and zeros must be [K/{group_size}, N]")
+    return (codes - np.repeat(z, group_size, axis=0)).astype(np.float32) * np.repeat(s, group_size, axis=0)
+
+
 def w4a16_reference(a: np.ndarray, qweight: np.ndarray, scales: np.ndarray,
                     group_size: int = 128, out_dtype: str | None = None) -> np.ndarray:
     """``a.float() @ dequant(W)`` with fp32 accumulation (tests/test_marlin_int4.py:49).
@@ -76,6 +91,12 @@ def w4a16_reference(a: np.ndarray, qweight: np.ndarray, scales: np.ndarray,
     deq = dequant_int4(qweight, scales, group_size)
     out = np.asarray(a, dtype=np.float32) @ deq
     return round_to(out, out_dtype) if out_dtype else out
+
+
+def w4a16_reference_zp(a: np.ndarray, qweight: np.ndarray, scales: np.ndarray, zeros: np.ndarray,
+                       group_size: int = 128) -> np.ndarray:
+    """``a.float() @ ((q - z) * s)`` with fp32 accumulation (asymmetric checkpoints)."""
+    return np.asarray(a, dtype=np.float32) @ dequant_int4_zp(qweight, scales, zeros, group_size)
 
 
 def quantize_int4_rtn(weight_kn: np.ndarray, group_size: int = 128,

@@ -18,17 +18,25 @@ def test_unpack_along_k_and_n():
     assert np.array_equal(ck._unpack_words_n(_pack_n(codes, order), order).numpy(), codes)
 
 
-def test_asymmetric_zero_points_rejected():
+def test_zero_offset_host_side():
+    """(8 - z) * s per (group, column), fp32, with s rounded to the activation dtype;
+    None when every zero point is 8; GPTQ v1 storage (z - 1) and AWQ's word order
+    unpack to the same zero points; bad shapes and group maps are rejected."""
     k, n = 256, 64
+    rng = np.random.default_rng(3)
+    z = rng.integers(0, 16, (k // 128, n)).astype(np.uint8)
+    s = torch.from_numpy((rng.random((k // 128, n)) * 0.02 + 0.002).astype(np.float32))
+    zo = ck._zero_offset(torch.from_numpy(z.astype(np.int64)), s, torch.bfloat16, torch.device("cpu"))
+    want = (8 - z.astype(np.float64)) * s.to(torch.bfloat16).double().numpy()
+    assert zo.dtype == torch.float32 and np.array_equal(zo.double().numpy(), want)
+    assert ck._zero_offset(torch.full((2, n), 8), s, torch.float16, torch.device("cpu")) is None
+    with pytest.raises(ValueError):
+        ck._zero_offset(torch.full((2, n), 16), s, torch.float16, torch.device("cpu"))
+    v1 = np.clip(z.astype(np.int64) - 1, 0, 15)
+    assert np.array_equal((ck._unpack_words_n(_pack_n(v1)) + 1).numpy(), np.maximum(z, 1))
+    order = (0, 2, 4, 6, 1, 3, 5, 7)
+    assert np.array_equal(ck._unpack_words_n(_pack_n(z, order), order).numpy(), z)
     q = _pack_k(np.zeros((k, n), np.uint8))
-    s = torch.ones((k // 128, n), dtype=torch.float16)
-    zeros = np.full((k // 128, n), 7, np.uint8)  # v1 storage of zero point 8
-    zeros[1, 5] = 3
-    with pytest.raises(NotImplementedError):
-        ck.from_gptq(q, s, _pack_n(zeros))
-    with pytest.raises(NotImplementedError):
-        ck.from_awq(_pack_n(np.zeros((k, n), np.uint8), (0, 2, 4, 6, 1, 3, 5, 7)), s,
-                    _pack_n(np.full((k // 128, n), 5, np.uint8)))
     with pytest.raises(ValueError):
         ck.from_gptq(q, s, g_idx=torch.zeros(k, dtype=torch.int32))  # every row in group 0
     with pytest.raises(ValueError):

@@ -93,3 +93,28 @@ def test_torch_pack_matches_oracle_pack():
     from torchinferno_amd.kernels import int4 as ti4
     codes = torch.randint(0, 16, (64, 24), generator=torch.Generator().manual_seed(5))
     assert np.array_equal(ti4.pack_int4(codes).numpy(), o.pack_int4(codes.numpy().astype(np.uint8)))
+
+
+def test_zero_point_dequant_closed_forms():
+    """(q - z) * s: z = 8 is the symmetric dequant; q = z gives exact zeros; each
+    group's zero point acts only on its own 128 rows and column."""
+    rng = np.random.default_rng(11)
+    k, n = 256, 24
+    codes = rng.integers(0, 16, (k, n), dtype=np.uint8)
+    q = o.pack_int4(codes)
+    s = torch.from_numpy((rng.random((2, n)) * 0.02 + 0.002).astype(np.float32)).to(torch.bfloat16).float().numpy()
+    z8 = np.full((2, n), 8, np.int32)
+    assert np.array_equal(o.dequant_int4_zp(q, s, z8), o.dequant_int4(q, s))
+    z = rng.integers(0, 16, (2, n)).astype(np.int32)
+    deq = o.dequant_int4_zp(q, s, z)
+    for g in range(2):
+        rows = slice(128 * g, 128 * (g + 1))
+        want = (codes[rows].astype(np.float64) - z[g]) * s[g].astype(np.float64)
+        assert np.array_equal(deq[rows].astype(np.float64), want)
+    z2 = z.copy()
+    z2[1, 3] += 1
+    diff = o.dequant_int4_zp(q, s, z2) - deq
+    assert np.all(diff[128:, 3] == -s[1, 3]) and np.count_nonzero(diff) == 128
+    a = rng.standard_normal((3, k)).astype(np.float32)
+    np.testing.assert_allclose(o.w4a16_reference_zp(a, q, s, z),
+                               a.astype(np.float64) @ deq.astype(np.float64), rtol=1e-5, atol=1e-5)

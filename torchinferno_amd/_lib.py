@@ -42,6 +42,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ti_w4a16_gemm": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ti_w4a16_gemm_noalloc": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "ti_w4a16_noalloc_scratch_bytes": (_sz, []),
+    "ti_w4a16_zero_point_add": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp]),
     "ti_w4a16_plan_name": (_i, [_i, _i, _i, _i, ctypes.c_char_p, _sz]),
     "ti_fp8_quant_per_token": (_i, [_vp, _i, _i, _i, _f, _vp, _vp, _vp]),
     "ti_fp8_quant_weight_per_channel": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
