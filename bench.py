@@ -424,6 +424,35 @@ def fp8_single_point(spec, launches, dev, stream):
     print(json.dumps({"point": spec, "launches": launches}), flush=True)
 
 
+def moe_single_point(t, launches, dev, stream):
+    """Launch the config-4 routed FP8 MoE (router included) at T tokens `launches`
+    times: the program a kernel-trace run profiles."""
+    import torch
+    from torchinferno_amd import _lib
+    L = _lib.lib()
+    e, h, inter, k = 256, 7168, 2048, 8
+    w13 = torch.randint(-120, 120, (e, 2 * inter, h), device=dev, dtype=torch.int8)
+    w2 = torch.randint(-120, 120, (e, h, inter), device=dev, dtype=torch.int8)
+    s13 = torch.rand((e, 2 * inter // 128, h // 128), device=dev) * 1e-3 + 1e-4
+    s2 = torch.rand((e, h // 128, inter // 128), device=dev) * 1e-3 + 1e-4
+    x = torch.randn((t, h), device=dev).to(torch.bfloat16)
+    logits = torch.randn((t, e), device=dev)
+    wts = torch.empty((t, k), dtype=torch.float32, device=dev)
+    ids = torch.empty((t, k), dtype=torch.int32, device=dev)
+    out = torch.empty((t, h), dtype=torch.bfloat16, device=dev)
+    need = int(L.ti_fp8_moe_workspace_bytes(t, k, e, h, inter))
+    ws = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+    wsp = (ws.data_ptr() + 255) & ~255
+    for _ in range(launches):
+        _check("route", L.ti_moe_route_topk(logits.data_ptr(), t, e, k, 1, 1.0, wts.data_ptr(), ids.data_ptr(),
+                                            stream))
+        _check("moe", L.ti_fp8_moe(x.data_ptr(), wts.data_ptr(), ids.data_ptr(), t, k, w13.data_ptr(),
+                                   s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), e, h, inter, 0.0, 0,
+                                   out.data_ptr(), wsp, need, stream))
+    torch.cuda.synchronize()
+    print(json.dumps({"point": f"moe:{t}", "launches": launches}), flush=True)
+
+
 # --------------------------------------------------------------------------- fused producers
 
 
@@ -578,6 +607,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"point": "copy", "bytes_read": src.numel() * 4, "launches": args.steps}), flush=True)
+        return
+    if args.point and args.point.startswith("moe:"):
+        moe_single_point(int(args.point.split(":")[1]), args.steps, dev, stream)
         return
     if args.point and args.point.count(":") == 2:
         fp8_single_point(args.point, args.steps, dev, stream)

@@ -15,11 +15,11 @@
 //
 // Pipeline (one stream, no host synchronisation, graph-capturable):
 //   1. act_quant of the T hidden rows (1x128, shared by all k routes of a row);
-//   2. align: one workgroup counts routes per expert, prefix-sums them, assigns
-//      every route a row in expert-sorted order and writes the grouped GEMM's
-//      m-tile table (expert, first row, rows) -- rows inside an expert are
-//      placed by LDS atomics, which changes no value because every output row
-//      of the GEMMs depends only on its own input row;
+//   2. align: routes counted per expert, prefix-summed, every route assigned a
+//      row in expert-sorted order, and the grouped GEMM's m-tile table
+//      (expert, first row, rows) written -- rows inside an expert are placed by
+//      atomics, which changes no value because every output row of the GEMMs
+//      depends only on its own input row;
 //   3. grouped GEMM w13 (gathering hidden rows by token) -> [R, 2I] bf16;
 //   4. SwiGLU x route weight -> bf16 -> 1x128 quant, per sorted row;
 //   5. grouped GEMM w2 -> [R, H] bf16;
@@ -143,13 +143,15 @@ struct Ws {
   int* tok_of_pos;                         // [R] token of sorted row p
   int* route_of_pos;                       // [R] route of sorted row p
   int* tile_expert; int* tile_row0; int* tile_rows; int* num_tiles;
+  int* cnt;                                // [2E]: routes per expert, then the placement cursors
+  int* row0;                               // [E] first sorted row of each expert
   uint16_t* out1;                          // [R, 2I] bf16
   uint8_t* hq; float* hs;                  // [R, I] e4m3, [R, I/128]
   uint16_t* out2;                          // [R, H] bf16
   size_t bytes;
 };
 
-Ws carve(uint8_t* base, int T, int k, int H, int I, const Plan& p) {
+Ws carve(uint8_t* base, int T, int k, int E, int H, int I, const Plan& p) {
   const size_t R = (size_t)T * k;
   size_t off = 0;
   auto take = [&](size_t n) {
@@ -167,6 +169,8 @@ Ws carve(uint8_t* base, int T, int k, int H, int I, const Plan& p) {
   w.tile_row0 = (int*)take((size_t)p.max_tiles * 4);
   w.tile_rows = (int*)take((size_t)p.max_tiles * 4);
   w.num_tiles = (int*)take(4);
+  w.cnt = (int*)take((size_t)2 * E * 4);
+  w.row0 = (int*)take((size_t)E * 4);
   w.out1 = (uint16_t*)take(R * 2 * I * 2);
   w.hq = take(R * I);
   w.hs = (float*)take(R * (I / 128) * 4);
@@ -175,57 +179,96 @@ Ws carve(uint8_t* base, int T, int k, int H, int I, const Plan& p) {
   return w;
 }
 
-// One workgroup: routes -> expert-sorted rows and the m-tile table.
-__global__ __launch_bounds__(kAlignThreads) void align_kernel(const int* __restrict__ ids, int R, int E, int bm,
-                                                              int* __restrict__ pos_of_route,
-                                                              int* __restrict__ tok_of_pos,
-                                                              int* __restrict__ route_of_pos, int k,
-                                                              int* __restrict__ tile_expert,
-                                                              int* __restrict__ tile_row0,
-                                                              int* __restrict__ tile_rows,
-                                                              int* __restrict__ num_tiles) {
-  __shared__ int cnt[kMaxExperts];
-  __shared__ int off[kMaxExperts];
-  __shared__ int toff[kMaxExperts];
-  for (int e = threadIdx.x; e < E; e += kAlignThreads) cnt[e] = 0;
+// Routes -> expert-sorted rows and the m-tile table, in three launches over
+// the R = T*k routes (no single-workgroup pass over them):
+//   align_count: per-workgroup LDS histogram of expert ids, added to cnt[E];
+//   align_scan:  one workgroup: prefix sums of cnt -> first row and first
+//                m-tile of every expert, the m-tile table, and the cursors;
+//   align_place: every route takes the next row of its expert (a global
+//                atomic on the expert's cursor) and records the row <-> route
+//                maps.
+// Rows inside an expert are placed in arrival order, which changes no value:
+// every output row of the grouped GEMMs depends only on its own input row, and
+// the combine sums a token's routes in expert order.  cnt and cursors start at
+// zero: align_zero clears them (a kernel, not a memset, so graph replays clear
+// them too).
+constexpr int kAlignBlock = 256;
+
+__global__ __launch_bounds__(kAlignBlock) void align_zero_kernel(int* __restrict__ cnt, int E) {
+  for (int e = blockIdx.x * kAlignBlock + threadIdx.x; e < 2 * E; e += gridDim.x * kAlignBlock) cnt[e] = 0;
+}
+
+__global__ __launch_bounds__(kAlignBlock) void align_count_kernel(const int* __restrict__ ids, int R, int E,
+                                                                  int* __restrict__ cnt) {
+  __shared__ int h[kMaxExperts];
+  for (int e = threadIdx.x; e < E; e += kAlignBlock) h[e] = 0;
   __syncthreads();
-  for (int r = threadIdx.x; r < R; r += kAlignThreads) {
+  const int r = blockIdx.x * kAlignBlock + threadIdx.x;
+  if (r < R) {
     const int e = ids[r];
-    pos_of_route[r] = (e >= 0 && e < E) ? atomicAdd(&cnt[e], 1) : -1;
+    if (e >= 0 && e < E) atomicAdd(&h[e], 1);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int rows = 0, tiles = 0;
-    for (int e = 0; e < E; ++e) {
-      off[e] = rows;
-      toff[e] = tiles;
-      rows += cnt[e];
-      tiles += (cnt[e] + bm - 1) / bm;
-    }
-    *num_tiles = tiles;
-  }
+  for (int e = threadIdx.x; e < E; e += kAlignBlock)
+    if (h[e]) atomicAdd(&cnt[e], h[e]);
+}
+
+// One workgroup of kAlignThreads: exclusive scans of rows and m-tiles over E <= 1024.
+__global__ __launch_bounds__(kAlignThreads) void align_scan_kernel(const int* __restrict__ cnt, int E, int bm,
+                                                                   int* __restrict__ row0, int* __restrict__ tile_expert,
+                                                                   int* __restrict__ tile_row0,
+                                                                   int* __restrict__ tile_rows,
+                                                                   int* __restrict__ num_tiles) {
+  __shared__ int srow[kMaxExperts], stile[kMaxExperts];
+  const int e = threadIdx.x;
+  const int n = e < E ? cnt[e] : 0;
+  srow[e] = n;
+  stile[e] = (n + bm - 1) / bm;
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += kAlignThreads) {
-    const int n = cnt[e];
+  // Hillis-Steele inclusive scan over the 1024 slots
+  for (int off = 1; off < kMaxExperts; off <<= 1) {
+    const int a = e >= off ? srow[e - off] : 0, b = e >= off ? stile[e - off] : 0;
+    __syncthreads();
+    srow[e] += a;
+    stile[e] += b;
+    __syncthreads();
+  }
+  if (e < E) {
+    const int first = srow[e] - n, t0 = stile[e] - (n + bm - 1) / bm;
+    row0[e] = first;
     for (int j = 0; j * bm < n; ++j) {
-      tile_expert[toff[e] + j] = e;
-      tile_row0[toff[e] + j] = off[e] + j * bm;
-      tile_rows[toff[e] + j] = min(bm, n - j * bm);
+      tile_expert[t0 + j] = e;
+      tile_row0[t0 + j] = first + j * bm;
+      tile_rows[t0 + j] = min(bm, n - j * bm);
     }
   }
-  for (int r = threadIdx.x; r < R; r += kAlignThreads) {
-    const int local = pos_of_route[r];
-    if (local < 0) continue;
-    const int p = off[ids[r]] + local;
-    pos_of_route[r] = p;
-    tok_of_pos[p] = r / k;
-    route_of_pos[p] = r;
+  if (e == kMaxExperts - 1) *num_tiles = stile[e];
+}
+
+__global__ __launch_bounds__(kAlignBlock) void align_place_kernel(const int* __restrict__ ids, int R, int E, int k,
+                                                                  const int* __restrict__ row0,
+                                                                  int* __restrict__ cursor,
+                                                                  int* __restrict__ pos_of_route,
+                                                                  int* __restrict__ tok_of_pos,
+                                                                  int* __restrict__ route_of_pos) {
+  const int r = blockIdx.x * kAlignBlock + threadIdx.x;
+  if (r >= R) return;
+  const int e = ids[r];
+  if (e < 0 || e >= E) {
+    pos_of_route[r] = -1;
+    return;
   }
+  const int p = row0[e] + atomicAdd(&cursor[e], 1);
+  pos_of_route[r] = p;
+  tok_of_pos[p] = r / k;
+  route_of_pos[p] = r;
 }
 
 // h = bf16(w * silu(g) * u) over one sorted row's 128-wide block, then 1x128
-// e4m3 quant (act_quant; power-of-two scales when round_scale).  One wave per (row, four blocks); rows past the
-// routed count are skipped.
+// e4m3 quant (act_quant; power-of-two scales when round_scale).  An item is
+// (row, four blocks): one wave, a 16-lane group per block, 8 elements (16-byte
+// loads) per lane; the launch has a wave per item (a grid-stride loop with a
+// capped grid measured slower: 155 vs 135 us at T=4096).
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __restrict__ gu, int I,
                                                            const float* __restrict__ route_w,
                                                            const int* __restrict__ route_of_pos,
@@ -234,56 +277,56 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
                                                            const int* __restrict__ tile_rows, long R,
                                                            float clamp_limit, int round_scale,
                                                            uint8_t* __restrict__ hq, float* __restrict__ hs) {
-  // One wave per (row, four 128-wide blocks); each 16-lane group owns a block,
-  // 8 elements (16-byte loads) per lane.
   const int lane = threadIdx.x & 63;
   const int IB = I / 128;
   const int QB = (IB + 3) / 4;
-  const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= R * QB) return;
-  const long p = item / QB;
-  const int blk = (int)(item % QB) * 4 + (lane >> 4);
-  // Rows in use: tile table end (last tile's row0 + rows).
+  // Rows in use: the tile table's end (last tile's row0 + rows).
   const int nt = *num_rows_tiles;
   const long used = nt > 0 ? (long)tile_row0[nt - 1] + tile_rows[nt - 1] : 0;
-  if (p >= used) return;
-  const bool on = blk < IB;
-  const float w = route_w[route_of_pos[p]];
-  const uint16_t* row = gu + p * 2 * I;
-  const int c = min(blk, IB - 1) * 128 + (lane & 15) * 8;
-  const uint4 gw = *(const uint4*)(row + c);
-  const uint4 uw = *(const uint4*)(row + I + c);
-  const uint32_t gv[4] = {gw.x, gw.y, gw.z, gw.w}, uv[4] = {uw.x, uw.y, uw.z, uw.w};
-  float h[8];
-  float amax = 0.f;
+  const long items = used * QB;
+  const long stride = (long)gridDim.x * 4;
+#pragma unroll 2
+  for (long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6); item < items; item += stride) {
+    const long p = item / QB;
+    const int blk = (int)(item % QB) * 4 + (lane >> 4);
+    const bool on = blk < IB;
+    const float w = route_w[route_of_pos[p]];
+    const uint16_t* row = gu + p * 2 * I;
+    const int c = min(blk, IB - 1) * 128 + (lane & 15) * 8;
+    const uint4 gw = *(const uint4*)(row + c);
+    const uint4 uw = *(const uint4*)(row + I + c);
+    const uint32_t gv[4] = {gw.x, gw.y, gw.z, gw.w}, uv[4] = {uw.x, uw.y, uw.z, uw.w};
+    float h[8];
+    float amax = 0.f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float g = bf16_bits_to_f32((uint16_t)(gv[i >> 1] >> (16 * (i & 1))));
-    float u = bf16_bits_to_f32((uint16_t)(uv[i >> 1] >> (16 * (i & 1))));
-    if (clamp_limit > 0.f) {
-      u = fminf(fmaxf(u, -clamp_limit), clamp_limit);
-      g = fminf(g, clamp_limit);
+    for (int i = 0; i < 8; ++i) {
+      float g = bf16_bits_to_f32((uint16_t)(gv[i >> 1] >> (16 * (i & 1))));
+      float u = bf16_bits_to_f32((uint16_t)(uv[i >> 1] >> (16 * (i & 1))));
+      if (clamp_limit > 0.f) {
+        u = fminf(fmaxf(u, -clamp_limit), clamp_limit);
+        g = fminf(g, clamp_limit);
+      }
+      const float act = g / (1.0f + expf(-g)) * u;
+      h[i] = bf16_bits_to_f32(f32_to_bf16_bits(w * act));
+      amax = fmaxf(amax, fabsf(h[i]));
     }
-    const float act = g / (1.0f + expf(-g)) * u;
-    h[i] = bf16_bits_to_f32(f32_to_bf16_bits(w * act));
-    amax = fmaxf(amax, fabsf(h[i]));
-  }
-  // block max over the 16 lanes of the group
+    // block max over the 16 lanes of the group
 #pragma unroll
-  for (int o = 1; o < 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-  amax = fmaxf(amax, 1e-4f);
-  float s = amax * (1.0f / kE4M3Max);
-  if (round_scale) {  // 2^ceil(log2(amax / 448)), the ue8m0 scale format
-    const uint32_t b = __float_as_uint(s);
-    const int e = (int)((b >> 23) & 0xFF) - 127 + ((b & 0x7FFFFFu) != 0 ? 1 : 0);
-    s = __uint_as_float((uint32_t)(e + 127) << 23);
-  }
-  float y[8];
+    for (int o = 1; o < 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    amax = fmaxf(amax, 1e-4f);
+    float sc = amax * (1.0f / kE4M3Max);
+    if (round_scale) {  // 2^ceil(log2(amax / 448)), the ue8m0 scale format
+      const uint32_t bits = __float_as_uint(sc);
+      const int e = (int)((bits >> 23) & 0xFF) - 127 + ((bits & 0x7FFFFFu) != 0 ? 1 : 0);
+      sc = __uint_as_float((uint32_t)(e + 127) << 23);
+    }
+    float y[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) y[i] = fminf(fmaxf(h[i] / s, -kE4M3Max), kE4M3Max);
-  if (on) {
-    *(uint2*)(hq + p * I + c) = fp8::e4m3_pack8_hw(y);
-    if ((lane & 15) == 0) hs[p * IB + blk] = s;
+    for (int i = 0; i < 8; ++i) y[i] = fminf(fmaxf(h[i] / sc, -kE4M3Max), kE4M3Max);
+    if (on) {
+      *(uint2*)(hq + p * I + c) = fp8::e4m3_pack8_hw(y);
+      if ((lane & 15) == 0) hs[p * IB + blk] = sc;
+    }
   }
 }
 
@@ -354,8 +397,8 @@ static bool moe_shape_ok(int T, int k, int E, int H, int I) {
 extern "C" size_t ti_fp8_moe_workspace_bytes(int T, int k, int E, int H, int I) {
   if (!moe_shape_ok(T, k, E, H, I) || T == 0) return 0;
   // One size serves both weight formats (their plans may pick different tiles).
-  const size_t b1 = carve(nullptr, T, k, H, I, make_plan(T, k, E, 1)).bytes;
-  const size_t b2 = carve(nullptr, T, k, H, I, make_plan(T, k, E, 2)).bytes;
+  const size_t b1 = carve(nullptr, T, k, E, H, I, make_plan(T, k, E, 1)).bytes;
+  const size_t b2 = carve(nullptr, T, k, E, H, I, make_plan(T, k, E, 2)).bytes;
   return b1 > b2 ? b1 : b2;
 }
 
@@ -375,13 +418,13 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
                "%s: hidden, w13, w2 must be 16-byte and out, scales 4-byte aligned", name);
   if (T == 0) return TI_OK;
   Plan p = make_plan(T, k, E, smode);
-  Ws w = carve(nullptr, T, k, H, I, p);
+  Ws w = carve(nullptr, T, k, E, H, I, p);
   if (!workspace || workspace_bytes < w.bytes) {
     set_error("%s: workspace of %zu bytes required (got %zu)", name, w.bytes, workspace_bytes);
     return TI_ERR_WORKSPACE;
   }
   TI_CHECK_ARG(((uintptr_t)workspace & 255) == 0, "%s: workspace must be 256-byte aligned", name);
-  w = carve((uint8_t*)workspace, T, k, H, I, p);
+  w = carve((uint8_t*)workspace, T, k, E, H, I, p);
   const long R = (long)T * k;
   const bool f4 = smode == 2;
 
@@ -389,9 +432,15 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
   int st = ti_fp8_quant_block(hidden, TI_DTYPE_BF16, T, H, 128, round_scale ? 1 : 0, w.xq, w.xs, 0, stream);
   if (st != TI_OK) return st;
   // 2. align
-  hipLaunchKernelGGL(align_kernel, dim3(1), dim3(kAlignThreads), 0, stream, (const int*)topk_ids, (int)R, E, p.bm,
-                     w.pos_of_route, w.tok_of_pos, w.route_of_pos, k, w.tile_expert, w.tile_row0, w.tile_rows,
-                     w.num_tiles);
+  const unsigned rblocks = (unsigned)((R + kAlignBlock - 1) / kAlignBlock);
+  hipLaunchKernelGGL(align_zero_kernel, dim3((unsigned)((2 * E + kAlignBlock - 1) / kAlignBlock)), dim3(kAlignBlock),
+                     0, stream, w.cnt, E);
+  hipLaunchKernelGGL(align_count_kernel, dim3(rblocks), dim3(kAlignBlock), 0, stream, (const int*)topk_ids, (int)R,
+                     E, w.cnt);
+  hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(kAlignThreads), 0, stream, (const int*)w.cnt, E, p.bm,
+                     w.row0, w.tile_expert, w.tile_row0, w.tile_rows, w.num_tiles);
+  hipLaunchKernelGGL(align_place_kernel, dim3(rblocks), dim3(kAlignBlock), 0, stream, (const int*)topk_ids, (int)R,
+                     E, k, (const int*)w.row0, w.cnt + E, w.pos_of_route, w.tok_of_pos, w.route_of_pos);
   TI_CHECK_LAUNCH("moe(align)");
   // 3. grouped w13: [R, 2I] = xq[tok] . w13[e]^T
   fp8::GemmArgs g{};
@@ -409,7 +458,9 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
   TI_CHECK_LAUNCH("moe(w13)");
   // 4. swiglu x route weight -> 1x128 quant
   const long items = R * ((I / 128 + 3) / 4);
-  hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, w.out1, I,
+  const long sw_blocks = (items + 3) / 4;
+  hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)sw_blocks), dim3(256), 0, stream,
+                     w.out1, I,
                      topk_weights, w.route_of_pos, w.num_tiles, w.tile_row0, w.tile_rows, R, clamp_limit,
                      round_scale, w.hq, w.hs);
   TI_CHECK_LAUNCH("moe(swiglu)");
