@@ -284,22 +284,33 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
   // association, so the same results.  pd/sd: the deferred partials and
   // scales (zero before the first step: acc + 0*0 = acc).
   constexpr bool DEFER = SMODE >= 1 && FM * FN * MM::NACC <= 32;
-  acc_t pd[DEFER ? FM : 1][DEFER ? FN : 1];
-  float sd[DEFER ? FM : 1][MM::NACC];
+  // Block mode with deferred folds forms the row-scale products once per
+  // wave in LDS (the wave's TM products, one per lane) rather than once per
+  // accumulator row in every lane.
+  constexpr bool LDS_PROD = SMODE == 1 && DEFER && FM * MM::NACC >= 16;
+  // Two buffers, alternated by the parity of the step (a compile-time index:
+  // the K loop is unrolled by two), so no register copies carry them over.
+  acc_t pd[DEFER ? 2 : 1][DEFER ? FM : 1][DEFER ? FN : 1];
+  float sd[DEFER ? 2 : 1][DEFER ? FM : 1][MM::NACC];
 #pragma unroll
-  for (int i = 0; i < (DEFER ? FM : 1); ++i) {
+  for (int q = 0; q < (DEFER ? 2 : 1); ++q)
 #pragma unroll
-    for (int e = 0; e < MM::NACC; ++e) sd[i][e] = 0.f;
+    for (int i = 0; i < (DEFER ? FM : 1); ++i) {
 #pragma unroll
-    for (int j = 0; j < (DEFER ? FN : 1); ++j)
+      for (int e = 0; e < MM::NACC; ++e) sd[q][i][e] = 0.f;
 #pragma unroll
-      for (int e = 0; e < MM::NACC; ++e) pd[i][j][e] = 0.f;
-  }
-  auto fold = [&](int fm, int fn, const acc_t& p, const float (&srow)[MM::NACC]) {
+      for (int j = 0; j < (DEFER ? FN : 1); ++j)
+#pragma unroll
+        for (int e = 0; e < MM::NACC; ++e) pd[q][i][j][e] = 0.f;
+    }
+  // Step parity Q: fold the other buffer (the previous step), keep this one.
+  auto fold = [&](auto Q, int fm, int fn, const acc_t& p, const float (&srow)[MM::NACC]) {
+    constexpr int q = decltype(Q)::value;
     if constexpr (DEFER) {
 #pragma unroll
-      for (int e = 0; e < MM::NACC; ++e) acc[fm][fn][e] = __builtin_fmaf(pd[fm][fn][e], sd[fm][e], acc[fm][fn][e]);
-      pd[fm][fn] = p;
+      for (int e = 0; e < MM::NACC; ++e)
+        acc[fm][fn][e] = __builtin_fmaf(pd[1 - q][fm][fn][e], sd[1 - q][fm][e], acc[fm][fn][e]);
+      pd[q][fm][fn] = p;
     } else {
 #pragma unroll
       for (int e = 0; e < MM::NACC; ++e) acc[fm][fn][e] = __builtin_fmaf(p[e], srow[e], acc[fm][fn][e]);
@@ -309,7 +320,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
   const int arow0 = wm * TM + (lane % MF);
   const int brow0 = wn * TN + (lane % MF);
 
-  for (int i = 0; i < nsteps; ++i) {
+  // Step i reads ring stage i % R, at byte offset soff (kept by the caller).
+  auto step = [&](int i, int soff, auto Q) {
+    constexpr int q = decltype(Q)::value;
     if (i + P - 1 < nsteps) {
       if constexpr (P > 1) {
         if (n_mine > NI_LO) wait_vm_barrier<(P - 1) * NI_HI>();
@@ -322,7 +335,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
     }
     if (i + P < nsteps) issue(i + P);
 
-    const uint8_t* st = smem + (i % R) * STAGE;
+    const uint8_t* st = smem + soff;
     const uint8_t* sA = st;
     const uint8_t* sB = st + A_BYTES;
     if constexpr (SMODE == 0) {
@@ -392,15 +405,25 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
           for (int ks = 0; ks < KS; ++ks) pf[fn] = MM::mma4(af[ks], bf[ks][fn], pf[fn], eb[ks][fn]);
         }
 #pragma unroll
-        for (int fn = 0; fn < FN; ++fn) fold(fm, fn, pf[fn], srow);
+        for (int fn = 0; fn < FN; ++fn) fold(Q, fm, fn, pf[fn], srow);
         if constexpr (DEFER) {
 #pragma unroll
-          for (int e = 0; e < MM::NACC; ++e) sd[fm][e] = srow[e];
+          for (int e = 0; e < MM::NACC; ++e) sd[q][fm][e] = srow[e];
         }
       }
     } else {
       const float* sS = (const float*)(st + A_BYTES + B_BYTES);
       const float sbv = sS[NI_SA * 64 + (wn * TN) / 128];
+      // LDS_PROD: the wave's TM row scales times its column block's scale,
+      // one product per lane, through the wave's own LDS slot (a wave's LDS
+      // accesses complete in order, so its reads below see its writes).
+      float* wsc = (float*)(smem + R * STAGE) + wave * TM;
+      if constexpr (LDS_PROD) {
+#pragma unroll
+        for (int j = 0; j < TM; j += 64)
+          if (TM % 64 == 0 || j + lane < TM) wsc[j + lane] = sS[wm * TM + j + lane] * sbv;
+        __builtin_amdgcn_wave_barrier();
+      }
       // All B fragments of the step stay in registers; A is read one M tile
       // at a time (bounds register use with the per-tile partial sums).
       i32x8 bf[KS][FN];
@@ -428,7 +451,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
         }
         float srow[MM::NACC];
 #pragma unroll
-        for (int e = 0; e < MM::NACC; ++e) srow[e] = sS[wm * TM + fm * MF + MM::row(e, lane)] * sbv;
+        for (int e = 0; e < MM::NACC; ++e)
+          srow[e] = LDS_PROD ? wsc[fm * MF + MM::row(e, lane)] : sS[wm * TM + fm * MF + MM::row(e, lane)] * sbv;
         // All FN partial sums first, then their folds: each fold then
         // waits only on its own MFMA chain, the later chains still running.
         acc_t pf[FN];
@@ -440,21 +464,45 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
           for (int ks = 0; ks < KS; ++ks) pf[fn] = MM::mma(af[ks], bf[ks][fn], pf[fn]);
         }
 #pragma unroll
-        for (int fn = 0; fn < FN; ++fn) fold(fm, fn, pf[fn], srow);
+        for (int fn = 0; fn < FN; ++fn) fold(Q, fm, fn, pf[fn], srow);
         if constexpr (DEFER) {
 #pragma unroll
-          for (int e = 0; e < MM::NACC; ++e) sd[fm][e] = srow[e];
+          for (int e = 0; e < MM::NACC; ++e) sd[q][fm][e] = srow[e];
         }
       }
     }
-  }
+  };
+  auto next_stage = [](int soff) { return soff == (R - 1) * STAGE ? 0 : soff + STAGE; };
+  using Q0 = std::integral_constant<int, 0>;
+  using Q1 = std::integral_constant<int, 1>;
   if constexpr (DEFER) {
+    // Unrolled by two so the deferred buffers alternate at compile time; the
+    // last fold takes the buffer of the last step's parity.
+    auto fold_last = [&](auto Q) {
+      constexpr int q = decltype(Q)::value;
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
+      for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
+        for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-        for (int e = 0; e < MM::NACC; ++e) acc[fm][fn][e] = __builtin_fmaf(pd[fm][fn][e], sd[fm][e], acc[fm][fn][e]);
+          for (int e = 0; e < MM::NACC; ++e)
+            acc[fm][fn][e] = __builtin_fmaf(pd[q][fm][fn][e], sd[q][fm][e], acc[fm][fn][e]);
+    };
+    int i = 0, soff = 0;
+    for (; i + 1 < nsteps; i += 2) {
+      step(i, soff, Q0{});
+      soff = next_stage(soff);
+      step(i + 1, soff, Q1{});
+      soff = next_stage(soff);
+    }
+    if (i < nsteps) {
+      step(i, soff, Q0{});
+      fold_last(Q0{});
+    } else {
+      fold_last(Q1{});
+    }
+  } else {
+    for (int i = 0; i < nsteps; ++i) step(i, (i % R) * STAGE, Q0{});
   }
   wait_vm_all();
 
@@ -537,16 +585,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 //  17  BM=128 BN=256, 8 waves 2x4 (wave 64x64),   32x32 MFMA            128     3   -- MoE, ~128 rows/expert
 // The 8- and 16-wave kinds put two or four waves on each SIMD, which hides the
 // per-step barrier -> LDS read -> MFMA -> fold latency of one wave.
-template <int BM, int BN, int BK, int R, int SMODE>
+// Block mode adds, after the ring, each wave's TM scale products (WGN * BM
+// floats in all).
+template <int BM, int BN, int BK, int WGN, int R, int SMODE>
 constexpr int cfg_lds() {
   const int sa = SMODE >= 1 ? ((BM * 4 + 255) / 256) * 256 : 0;
   const int sb = SMODE == 1 ? 256 : (SMODE == 2 ? ((BN * 4 + 255) / 256) * 256 : 0);
-  return R * (BM * BK + BN * (SMODE == 2 ? BK / 2 : BK) + sa + sb);
+  return R * (BM * BK + BN * (SMODE == 2 ? BK / 2 : BK) + sa + sb) + (SMODE == 1 ? WGN * BM * 4 : 0);
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, int MF, int R, int SMODE, int ODT>
 void launch_cfg(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
-  constexpr int lds = cfg_lds<BM, BN, BK, R, SMODE>();
+  constexpr int lds = cfg_lds<BM, BN, BK, WGN, R, SMODE>();
   static_assert(lds <= 160 * 1024, "tile configuration exceeds the 160 KiB LDS");
   dim3 grid(p.tiles_m * p.tiles_n, p.splits);
   if (p.splits > 1)
@@ -559,7 +609,7 @@ void launch_cfg(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
 
 template <int BM, int BN, int BK, int WGM, int WGN, int MF, int R, int SMODE>
 void launch_grouped_cfg(const GemmArgs& x, int max_mtiles, hipStream_t stream) {
-  constexpr int lds = cfg_lds<BM, BN, BK, R, SMODE>();
+  constexpr int lds = cfg_lds<BM, BN, BK, WGN, R, SMODE>();
   dim3 grid((unsigned)(max_mtiles * x.tiles_n), 1);
   hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, BK, WGM, WGN, MF, R, SMODE, 0, TI_DTYPE_BF16>), grid,
                      dim3(64 * WGM * WGN), lds, stream, x);
