@@ -111,9 +111,12 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
 }
 
 struct Plan {
-  int kind;       // grouped GEMM tile kind
-  int bm;         // its m-tile rows
-  int max_tiles;  // m-tile table capacity
+  int kind;        // grouped GEMM tile kind
+  int bm;          // its m-tile rows
+  int max_tiles;   // m-tile table capacity
+  int kind2;       // second tier (-1: none): 256-row m-tiles for experts with more than bm rows
+  int bm2;         // its m-tile rows (0: no second tier)
+  int max_tiles2;  // second-tier table capacity
 };
 
 Plan make_plan(int T, int k, int E, int smode) {
@@ -129,10 +132,27 @@ Plan make_plan(int T, int k, int E, int smode) {
   const char* env = getenv("TI_ROCM_MOE_KIND");
   if (env && *env) {
     const int kk = atoi(env);
-    if (kk == 2 || kk == 5 || kk == 6 || kk == 9 || kk == 11 || kk == 12 || kk == 13 || kk == 15 || kk == 17) p.kind = kk;
+    if (kk == 2 || kk == 5 || kk == 6 || kk == 9 || kk == 11 || kk == 12 || kk == 13 || kk == 15 || kk == 16 || kk == 17) p.kind = kk;
   }
   p.bm = fp8::grouped_bm(p.kind);
   p.max_tiles = (int)(R / p.bm + E + 1);
+  // Two tiers with the 128-row tile: an expert's rows go to 256-row tiles,
+  // and a remainder of at most 128 rows to one 128-row tile.  An expert with
+  // 129-256 rows then streams its weights once (one 256-row tile) instead of
+  // once per 128-row tile.
+  p.kind2 = -1;
+  p.bm2 = 0;
+  p.max_tiles2 = 0;
+  if (p.kind == 17) {
+    const char* e2 = getenv("TI_ROCM_MOE_KIND2");
+    p.kind2 = (e2 && *e2) ? atoi(e2) : 16;
+    if (p.kind2 != 9 && p.kind2 != 16) p.kind2 = -1;
+  }
+  if (p.kind2 >= 0) {
+    p.bm2 = fp8::grouped_bm(p.kind2);
+    p.max_tiles = E + 1;
+    p.max_tiles2 = (int)(R / p.bm2 + E + 1);
+  }
   return p;
 }
 
@@ -143,6 +163,8 @@ struct Ws {
   int* tok_of_pos;                         // [R] token of sorted row p
   int* route_of_pos;                       // [R] route of sorted row p
   int* tile_expert; int* tile_row0; int* tile_rows; int* num_tiles;
+  int* tile2_expert; int* tile2_row0; int* tile2_rows; int* num_tiles2;  // second tier
+  int* num_rows;                           // device scalar: sorted rows in use
   int* cnt;                                // [2E]: routes per expert, then the placement cursors
   int* row0;                               // [E] first sorted row of each expert
   uint16_t* out1;                          // [R, 2I] bf16
@@ -169,6 +191,11 @@ Ws carve(uint8_t* base, int T, int k, int E, int H, int I, const Plan& p) {
   w.tile_row0 = (int*)take((size_t)p.max_tiles * 4);
   w.tile_rows = (int*)take((size_t)p.max_tiles * 4);
   w.num_tiles = (int*)take(4);
+  w.tile2_expert = (int*)take((size_t)p.max_tiles2 * 4);
+  w.tile2_row0 = (int*)take((size_t)p.max_tiles2 * 4);
+  w.tile2_rows = (int*)take((size_t)p.max_tiles2 * 4);
+  w.num_tiles2 = (int*)take(4);
+  w.num_rows = (int*)take(4);
   w.cnt = (int*)take((size_t)2 * E * 4);
   w.row0 = (int*)take((size_t)E * 4);
   w.out1 = (uint16_t*)take(R * 2 * I * 2);
@@ -213,36 +240,67 @@ __global__ __launch_bounds__(kAlignBlock) void align_count_kernel(const int* __r
     if (h[e]) atomicAdd(&cnt[e], h[e]);
 }
 
-// One workgroup of kAlignThreads: exclusive scans of rows and m-tiles over E <= 1024.
+// One workgroup of kAlignThreads: exclusive scans of rows and m-tiles over
+// E <= 1024.  With a second tier (bm2 > 0) an expert of n rows takes n / bm2
+// tiles of bm2 rows, the remainder r a further bm2 tile when r > bm and one
+// bm tile when 0 < r <= bm.
 __global__ __launch_bounds__(kAlignThreads) void align_scan_kernel(const int* __restrict__ cnt, int E, int bm,
-                                                                   int* __restrict__ row0, int* __restrict__ tile_expert,
+                                                                   int bm2, int* __restrict__ row0,
+                                                                   int* __restrict__ tile_expert,
                                                                    int* __restrict__ tile_row0,
                                                                    int* __restrict__ tile_rows,
-                                                                   int* __restrict__ num_tiles) {
-  __shared__ int srow[kMaxExperts], stile[kMaxExperts];
+                                                                   int* __restrict__ num_tiles,
+                                                                   int* __restrict__ tile2_expert,
+                                                                   int* __restrict__ tile2_row0,
+                                                                   int* __restrict__ tile2_rows,
+                                                                   int* __restrict__ num_tiles2,
+                                                                   int* __restrict__ num_rows) {
+  __shared__ int srow[kMaxExperts], stile[kMaxExperts], stile2[kMaxExperts];
   const int e = threadIdx.x;
   const int n = e < E ? cnt[e] : 0;
+  int n2 = 0, n1;  // second-tier and first-tier tiles of this expert
+  if (bm2 > 0) {
+    n2 = n / bm2;
+    const int r = n - n2 * bm2;
+    if (r > bm) ++n2;
+    n1 = (r > 0 && r <= bm) ? 1 : 0;
+  } else {
+    n1 = (n + bm - 1) / bm;
+  }
   srow[e] = n;
-  stile[e] = (n + bm - 1) / bm;
+  stile[e] = n1;
+  stile2[e] = n2;
   __syncthreads();
   // Hillis-Steele inclusive scan over the 1024 slots
   for (int off = 1; off < kMaxExperts; off <<= 1) {
-    const int a = e >= off ? srow[e - off] : 0, b = e >= off ? stile[e - off] : 0;
+    const int a = e >= off ? srow[e - off] : 0, b = e >= off ? stile[e - off] : 0,
+              c = e >= off ? stile2[e - off] : 0;
     __syncthreads();
     srow[e] += a;
     stile[e] += b;
+    stile2[e] += c;
     __syncthreads();
   }
   if (e < E) {
-    const int first = srow[e] - n, t0 = stile[e] - (n + bm - 1) / bm;
+    const int first = srow[e] - n, t0 = stile[e] - n1, u0 = stile2[e] - n2;
     row0[e] = first;
-    for (int j = 0; j * bm < n; ++j) {
+    for (int j = 0; j < n2; ++j) {
+      tile2_expert[u0 + j] = e;
+      tile2_row0[u0 + j] = first + j * bm2;
+      tile2_rows[u0 + j] = min(bm2, n - j * bm2);
+    }
+    const int done = min(n, n2 * bm2);
+    for (int j = 0; j < n1; ++j) {
       tile_expert[t0 + j] = e;
-      tile_row0[t0 + j] = first + j * bm;
-      tile_rows[t0 + j] = min(bm, n - j * bm);
+      tile_row0[t0 + j] = first + done + j * bm;
+      tile_rows[t0 + j] = min(bm, n - done - j * bm);
     }
   }
-  if (e == kMaxExperts - 1) *num_tiles = stile[e];
+  if (e == kMaxExperts - 1) {
+    *num_tiles = stile[e];
+    *num_tiles2 = stile2[e];
+    *num_rows = srow[e];
+  }
 }
 
 __global__ __launch_bounds__(kAlignBlock) void align_place_kernel(const int* __restrict__ ids, int R, int E, int k,
@@ -272,18 +330,13 @@ __global__ __launch_bounds__(kAlignBlock) void align_place_kernel(const int* __r
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __restrict__ gu, int I,
                                                            const float* __restrict__ route_w,
                                                            const int* __restrict__ route_of_pos,
-                                                           const int* __restrict__ num_rows_tiles,
-                                                           const int* __restrict__ tile_row0,
-                                                           const int* __restrict__ tile_rows, long R,
+                                                           const int* __restrict__ num_rows, long R,
                                                            float clamp_limit, int round_scale,
                                                            uint8_t* __restrict__ hq, float* __restrict__ hs) {
   const int lane = threadIdx.x & 63;
   const int IB = I / 128;
   const int QB = (IB + 3) / 4;
-  // Rows in use: the tile table's end (last tile's row0 + rows).
-  const int nt = *num_rows_tiles;
-  const long used = nt > 0 ? (long)tile_row0[nt - 1] + tile_rows[nt - 1] : 0;
-  const long items = used * QB;
+  const long items = (long)*num_rows * QB;  // rows in use
   const long stride = (long)gridDim.x * 4;
 #pragma unroll 2
   for (long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6); item < items; item += stride) {
@@ -437,8 +490,9 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
                      0, stream, w.cnt, E);
   hipLaunchKernelGGL(align_count_kernel, dim3(rblocks), dim3(kAlignBlock), 0, stream, (const int*)topk_ids, (int)R,
                      E, w.cnt);
-  hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(kAlignThreads), 0, stream, (const int*)w.cnt, E, p.bm,
-                     w.row0, w.tile_expert, w.tile_row0, w.tile_rows, w.num_tiles);
+  hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(kAlignThreads), 0, stream, (const int*)w.cnt, E, p.bm, p.bm2,
+                     w.row0, w.tile_expert, w.tile_row0, w.tile_rows, w.num_tiles, w.tile2_expert, w.tile2_row0,
+                     w.tile2_rows, w.num_tiles2, w.num_rows);
   hipLaunchKernelGGL(align_place_kernel, dim3(rblocks), dim3(kAlignBlock), 0, stream, (const int*)topk_ids, (int)R,
                      E, k, (const int*)w.row0, w.cnt + E, w.pos_of_route, w.tok_of_pos, w.route_of_pos);
   TI_CHECK_LAUNCH("moe(align)");
@@ -455,13 +509,20 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
   g.b_expert_stride = f4 ? (long)I * H : (long)2 * I * H;
   g.sb_expert_stride = f4 ? (long)2 * I * H / 128 : (long)cdiv(2 * I, 128) * (H / 128);
   fp8::launch_gemm_grouped(p.kind, smode, g, p.max_tiles, stream);
+  if (p.kind2 >= 0) {
+    fp8::GemmArgs gb = g;
+    gb.tiles_n = cdiv(2 * I, fp8::grouped_bn(p.kind2));
+    gb.tile_expert = w.tile2_expert; gb.tile_row0 = w.tile2_row0; gb.tile_rows = w.tile2_rows;
+    gb.num_mtiles = w.num_tiles2;
+    fp8::launch_gemm_grouped(p.kind2, smode, gb, p.max_tiles2, stream);
+  }
   TI_CHECK_LAUNCH("moe(w13)");
   // 4. swiglu x route weight -> 1x128 quant
   const long items = R * ((I / 128 + 3) / 4);
   const long sw_blocks = (items + 3) / 4;
   hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)sw_blocks), dim3(256), 0, stream,
                      w.out1, I,
-                     topk_weights, w.route_of_pos, w.num_tiles, w.tile_row0, w.tile_rows, R, clamp_limit,
+                     topk_weights, w.route_of_pos, w.num_rows, R, clamp_limit,
                      round_scale, w.hq, w.hs);
   TI_CHECK_LAUNCH("moe(swiglu)");
   // 5. grouped w2: [R, H] = hq . w2[e]^T
@@ -474,6 +535,13 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
   g2.b_expert_stride = f4 ? (long)H * I / 2 : (long)H * I;
   g2.sb_expert_stride = f4 ? (long)H * I / 128 : (long)cdiv(H, 128) * (I / 128);
   fp8::launch_gemm_grouped(p.kind, smode, g2, p.max_tiles, stream);
+  if (p.kind2 >= 0) {
+    fp8::GemmArgs gb = g2;
+    gb.tiles_n = cdiv(H, fp8::grouped_bn(p.kind2));
+    gb.tile_expert = w.tile2_expert; gb.tile_row0 = w.tile2_row0; gb.tile_rows = w.tile2_rows;
+    gb.num_mtiles = w.num_tiles2;
+    fp8::launch_gemm_grouped(p.kind2, smode, gb, p.max_tiles2, stream);
+  }
   TI_CHECK_LAUNCH("moe(w2)");
   // 6. combine
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)T), dim3(256), 0, stream, w.out2, H, (const int*)topk_ids,
