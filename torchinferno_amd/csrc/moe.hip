@@ -389,23 +389,39 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
                                                       const int* __restrict__ pos_of_route, int k,
                                                       uint16_t* __restrict__ y) {
   const long t = blockIdx.x;
-  int pos[kMaxTopk], eid[kMaxTopk];
-  int n = 0;
-  for (int s = 0; s < k; ++s) {
-    const int p = pos_of_route[t * k + s];
-    if (p < 0) continue;
-    // insertion by expert id (stable for equal ids: slot order)
-    const int e = ids[t * k + s];
-    int j = n++;
-    while (j > 0 && eid[j - 1] > e) { eid[j] = eid[j - 1]; pos[j] = pos[j - 1]; --j; }
-    eid[j] = e;
-    pos[j] = p;
+  // The token's rows sorted by expert id (stable: slot order for equal ids),
+  // by one thread into LDS.
+  __shared__ int spos[kMaxTopk], eid[kMaxTopk];
+  __shared__ int sn;
+  if (threadIdx.x == 0) {
+    int n = 0;
+    for (int s = 0; s < k; ++s) {
+      const int p = pos_of_route[t * k + s];
+      if (p < 0) continue;
+      const int e = ids[t * k + s];
+      int j = n++;
+      while (j > 0 && eid[j - 1] > e) { eid[j] = eid[j - 1]; spos[j] = spos[j - 1]; --j; }
+      eid[j] = e;
+      spos[j] = p;
+    }
+    sn = n;
   }
+  __syncthreads();
+  const int n = sn;
+  int pos[kMaxTopk];
+#pragma unroll
+  for (int j = 0; j < kMaxTopk; ++j) pos[j] = j < n ? spos[j] : 0;
   for (int c = threadIdx.x * 8; c < H; c += 256 * 8) {
     float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < n; ++j) {
-      const uint4 v = *(const uint4*)(out2 + (long)pos[j] * H + c);
-      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+    // all of the token's rows in flight before the in-order sum
+    // (absent rows read as +0, which leaves a sum that starts at +0 unchanged)
+    uint4 v[kMaxTopk];
+#pragma unroll
+    for (int j = 0; j < kMaxTopk; ++j)
+      v[j] = j < n ? *(const uint4*)(out2 + (long)pos[j] * H + c) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int j = 0; j < kMaxTopk; ++j) {
+      const uint32_t vv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
       for (int i = 0; i < 8; ++i) a[i] += bf16_bits_to_f32((uint16_t)(vv[i >> 1] >> (16 * (i & 1))));
     }
