@@ -159,3 +159,37 @@ def test_mxfp4_moe_matches_oracle(dev, monkeypatch, t, k, kind):
     ref = omoe.moe_reference(x.float().cpu().numpy(), w.cpu().numpy(), ids.cpu().numpy(), experts,
                              linear=omoe.mxfp4_linear)
     assert _rel_err(y.float().cpu().numpy(), ref) <= TOL
+
+
+def test_mxfp4_moe_tile_boundaries(dev, monkeypatch):
+    """MXFP4 experts whose row counts sit on the m-tile boundaries: the two-tier
+    128-row tile (kind 17) against the single-tier 128x128 tile (kind 15, to a
+    bf16-rounding bound) and the oracle."""
+    from torchinferno_amd.kernels import moe as tmoe
+    counts = [0, 1, 128, 129, 255, 256, 257, 385]
+    e, h, inter = len(counts), 512, 256
+    ex = _mxfp4_experts(e, h, inter, 21, dev)
+    ids_np = np.concatenate([np.full(c, i, dtype=np.int32) for i, c in enumerate(counts)])
+    np.random.default_rng(5).shuffle(ids_np)
+    t = ids_np.size
+    g = torch.Generator(device=dev).manual_seed(8)
+    x = torch.randn((t, h), generator=g, device=dev).to(torch.bfloat16)
+    ids = torch.from_numpy(ids_np).to(dev).view(t, 1)
+    w = (torch.rand((t, 1), generator=g, device=dev) + 0.5).float()
+    ys = {}
+    for kind in ("17", "15"):
+        print(f"[fp4] moe tile boundaries kind={kind}", flush=True)
+        monkeypatch.setenv("TI_ROCM_MOE_KIND", kind)
+        ys[kind] = tmoe.fused_mxfp4_moe(x, w, ids, ex).float().cpu().numpy()
+
+    def rows(st):  # step-major [K/128, N, 4] -> checkpoint [N, K/32]
+        return st.permute(1, 0, 2).reshape(st.size(1), -1).cpu().numpy()
+    experts = [(ex.w13[i].cpu().numpy(), rows(ex.w13_scale[i]), ex.w2[i].cpu().numpy(), rows(ex.w2_scale[i]))
+               for i in range(e)]
+    ref = omoe.moe_reference(x.float().cpu().numpy(), w.cpu().numpy(), ids_np.reshape(t, 1), experts,
+                             linear=omoe.mxfp4_linear)
+    assert _rel_err(ys["17"], ref) <= TOL
+    for i, c in enumerate(counts):
+        r = ids_np == i
+        if r.any():
+            assert np.abs(ys["17"][r] - ys["15"][r]).max() <= 2 ** -7 * np.abs(ys["15"][r]).max(), c
