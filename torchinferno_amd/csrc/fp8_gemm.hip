@@ -508,40 +508,45 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 
   // ---- epilogue ----
   const int col_l = lane % MF;
-  if constexpr (SPLIT == 0) {
+  // Split-K: each split's fp32 partial of the tile goes to the tile's own
+  // BM x BN region of the workspace with device-coherent stores, and the last
+  // split of the tile to finish sums the splits in split order.  A tile whose
+  // rows all lie below M stores in the register layout (float i of lane l of
+  // wave w at (w * PER + i) * 64 + l: each store instruction writes 256
+  // contiguous bytes) and is summed back into the registers, then stored like
+  // an unsplit tile; a tile that overhangs M (small M) stores only its rows
+  // below M, row-major, and the last split sums and stores element-wise.
+  constexpr int PER = FM * FN * MM::NACC;  // accumulator floats per lane
+  if constexpr (SPLIT != 0) {
+    const int split = blockIdx.y;
+    const bool full = m0 + BM <= M;  // uniform over the workgroup and its splits
+    auto region = [&](int sp) { return x.partial + ((long)sp * gridDim.x + blockIdx.x) * ((long)BM * BN); };
+    const long lane_base = (long)wave * PER * 64 + lane;
+    if (full) {
+      float* mine = region(split) + lane_base;
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
+      for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn) {
-        const int col = n0 + wn * TN + fn * MF + col_l;
-        float sbn = 1.f;
-        if constexpr (SMODE == 0) sbn = col < N ? x.sb[(long)col * x.sb_stride] : 0.f;
+        for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-        for (int e = 0; e < MM::NACC; ++e) {
-          const int row = m0 + wm * TM + fm * MF + MM::row(e, lane);
-          if (row < Mlim && col < N) {
-            float v = acc[fm][fn][e];
-            if constexpr (SMODE == 0) v = v * x.sa[(long)row * x.sa_stride] * sbn;
-            x.out[(long)row * N + col] = out_bits<ODT>(v);
+          for (int e = 0; e < MM::NACC; ++e)
+            __hip_atomic_store(mine + ((fm * FN + fn) * MM::NACC + e) * 64, acc[fm][fn][e], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      float* mine = region(split);
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const int c = wn * TN + fn * MF + col_l;
+#pragma unroll
+          for (int e = 0; e < MM::NACC; ++e) {
+            const int r = wm * TM + fm * MF + MM::row(e, lane);
+            if (m0 + r < M)
+              __hip_atomic_store(mine + r * BN + c, acc[fm][fn][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
         }
-      }
-    return;
-  } else {
-    const long mn = (long)M * N;
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn) {
-        const int col = n0 + wn * TN + fn * MF + col_l;
-#pragma unroll
-        for (int e = 0; e < MM::NACC; ++e) {
-          const int row = m0 + wm * TM + fm * MF + MM::row(e, lane);
-          if (row < M && col < N)
-            __hip_atomic_store(&x.partial[split * mn + (long)row * N + col], acc[fm][fn][e],
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     int* ticket = x.tickets + blockIdx.x;
@@ -549,18 +554,56 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
       last_flag = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == x.splits - 1;
     __syncthreads();
     if (!last_flag) return;
-    const int rows = min(BM, M - m0), cols = min(BN, N - n0);
-    for (int e = threadIdx.x; e < rows * cols; e += 64 * W) {
-      const int row = m0 + e / cols, col = n0 + e % cols;
-      const long off = (long)row * N + col;
-      float v = 0.f;
-      for (int sp = 0; sp < x.splits; ++sp)
-        v += __hip_atomic_load(&x.partial[sp * mn + off], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if constexpr (SMODE == 0) v = v * x.sa[(long)row * x.sa_stride] * x.sb[(long)col * x.sb_stride];
-      x.out[off] = out_bits<ODT>(v);
+    if (!full) {
+      const int rows = M - m0, cols = min(BN, N - n0);
+      for (int e = threadIdx.x; e < rows * cols; e += 64 * W) {
+        const int r = e / cols, c = e % cols;
+        float v = 0.f;
+        for (int sp = 0; sp < x.splits; ++sp)
+          v += __hip_atomic_load(region(sp) + r * BN + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int row = m0 + r, col = n0 + c;
+        if constexpr (SMODE == 0) v = v * x.sa[(long)row * x.sa_stride] * x.sb[(long)col * x.sb_stride];
+        x.out[(long)row * N + col] = out_bits<ODT>(v);
+      }
+      if (threadIdx.x == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int e = 0; e < MM::NACC; ++e) acc[fm][fn][e] = 0.f;
+    for (int sp = 0; sp < x.splits; ++sp) {
+      const float* src = region(sp) + lane_base;
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int e = 0; e < MM::NACC; ++e)
+            acc[fm][fn][e] += __hip_atomic_load(src + ((fm * FN + fn) * MM::NACC + e) * 64, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
     }
     if (threadIdx.x == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int col = n0 + wn * TN + fn * MF + col_l;
+      float sbn = 1.f;
+      if constexpr (SMODE == 0) sbn = col < N ? x.sb[(long)col * x.sb_stride] : 0.f;
+#pragma unroll
+      for (int e = 0; e < MM::NACC; ++e) {
+        const int row = m0 + wm * TM + fm * MF + MM::row(e, lane);
+        if (row < Mlim && col < N) {
+          float v = acc[fm][fn][e];
+          if constexpr (SMODE == 0) v = v * x.sa[(long)row * x.sa_stride] * sbn;
+          x.out[(long)row * N + col] = out_bits<ODT>(v);
+        }
+      }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -777,9 +820,16 @@ void launch_gemm_grouped(int kind, int smode, const GemmArgs& x, int max_mtiles,
   else launch_grouped_smode<1>(kind, x, max_mtiles, stream);
 }
 
+// Split-K partials: every split's accumulators of every (whole) tile.
+static size_t gemm_partial_bytes(const GemmPlan& p) {
+  return p.splits > 1 ? (size_t)p.splits * p.tiles_m * p.tiles_n * kBM[p.kind] * kBN[p.kind] * sizeof(float) : 0;
+}
+
 size_t gemm_workspace_bytes(const GemmPlan& p, int M, int N) {
   if (p.splits <= 1) return 0;
-  const size_t part = (size_t)p.splits * M * N * sizeof(float);
+  (void)M;
+  (void)N;
+  const size_t part = gemm_partial_bytes(p);
   const size_t tick = ((size_t)p.tiles_m * p.tiles_n * sizeof(int) + 255) & ~(size_t)255;
   return part + tick + 256;
 }
@@ -857,7 +907,7 @@ extern "C" size_t ti_fp8_gemm_workspace_bytes_max(int max_m, int N, int K, int s
   for (int m = 1; m <= max_m; ++m) {
     GemmPlan p = make_gemm_plan(m, N, K, scale_mode);
     if (p.splits <= 1) continue;
-    const size_t part = (size_t)p.splits * m * N * sizeof(float);
+    const size_t part = gemm_partial_bytes(p);
     pmax = part > pmax ? part : pmax;
     tmax = gemm_ticket_bytes(p) > tmax ? gemm_ticket_bytes(p) : tmax;
   }
