@@ -734,35 +734,31 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   } else if (M <= 16) {
     // 8-wave 16x128 tiles: two waves per SIMD hide each other's per-step
     // LDS/MFMA latency (12-24% faster than the 4-wave tile at M=16).
+    // Below 128 column tiles split over K, four ways when that stays within
+    // 256 workgroups, else two (config-2 qkv M=16: 23 -> 17 us).
     p.kind = 11;
     const long t = tiles(16, 128);
-    splits = t >= 72 ? 1 : (int)(cdiv(256, (int)t) < 4 ? cdiv(256, (int)t) : 4);
+    if (t < 128) splits = t * 4 <= 256 ? 4 : 2;
   } else if (M <= 32) {
     p.kind = 12;
     splits = tiles(32, 128) >= 128 ? 1 : 2;
   } else if (M <= 64) {
-    // Measured per scale mode at the config-2/3 shapes: 64x128 8-wave tiles
-    // when they alone fill the CUs, else 32x128 (per-token FP8 and MXFP4) or
-    // 64x128 split over K (block FP8); deep K (>= 16384) prefers fewer splits.
-    const bool deep = K >= 16384;
-    if (tiles(64, 128) >= 128) {
-      p.kind = 13;
-    } else if (smode == 0) {
-      p.kind = deep ? 13 : 12;
-      splits = deep ? 4 : 1;
-    } else if (smode == 1) {
-      p.kind = 13;
-      splits = deep ? 1 : 2;
-    } else {
-      p.kind = 12;
-      splits = deep ? 1 : 2;
-    }
+    // 64x128 8-wave tiles; below 128 column tiles, split over K two or four
+    // ways, as many as keep the grid within 256 workgroups (config-2 qkv M=64:
+    // 29 -> 24 us; block FP8 K=18432 N=7168: 90 -> 31 us).
+    p.kind = 13;
+    const long t = tiles(64, 128);
+    if (t < 128) splits = t * 4 <= 256 ? 4 : 2;
   } else if (M <= 128) {
-    // 128x128 tiles when they fill the CUs (per-token and block FP8), else
-    // 8-wave 64x128, split over K when fewer than 160 tiles (4 ways for
-    // MXFP4 at deep K).
-    if (smode != 2 && tiles(128, 128) >= 128) {
+    // Per-token and block FP8: 4-wave 128x128 tiles from 256 of them, the
+    // 8-wave 128x128 tile split in two from 72 (config-2 qkv M=128: 36 -> 31
+    // us; config-3 a: 66 -> 55 us); else, and for MXFP4, 8-wave 64x128 split
+    // over K when fewer than 160 tiles (4 ways for MXFP4 at deep K).
+    if (smode != 2 && tiles(128, 128) >= 256) {
       p.kind = 2;
+    } else if (smode != 2 && tiles(128, 128) >= 72) {
+      p.kind = 15;
+      splits = 2;
     } else {
       p.kind = 13;
       splits = tiles(64, 128) >= 160 ? 1 : ((smode == 2 && K >= 16384) ? 4 : 2);
@@ -776,6 +772,11 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
     p.kind = smode == 0 ? 14 : 16;
   } else if (tiles(256, 128) >= (smode >= 1 ? 128 : 144)) {
     p.kind = 9;
+  } else if (smode == 0 && tiles(256, 128) >= 64) {
+    // per-token FP8 between 64 and 144 256x128 tiles: split over K in two
+    // (config-2 down M=512: 151 -> 140 us)
+    p.kind = 9;
+    splits = 2;
   } else {
     // 128x128 on 8 waves (64x32 wave tiles) -- 64x128 for MXFP4 when it gives
     // 192 tiles -- split over K up to 128 128x128 tiles.
