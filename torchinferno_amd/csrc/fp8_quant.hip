@@ -45,7 +45,10 @@ __device__ __forceinline__ uint2 pack8(const uint32_t (&c)[8]) {
                     c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24));
 }
 
-// One workgroup (256 threads) per row; K % 8 == 0.  RECIP forms the scale as
+// Workgroup (row, chunk) of 256 threads; K % 8 == 0.  Every workgroup of a row
+// reads the whole row for its max (the same value in each: max is exact), then
+// quantizes its gridDim.y-th share of the row -- few rows (decode, small M)
+// still spread over many workgroups.  RECIP forms the scale as
 // amax * fl32(1/448) -- what torch computes for ``amax.float() / 448.0`` on a GPU
 // tensor (a host-scalar divisor becomes a reciprocal multiply), the per-channel
 // weight quant of fp8.py:129-138 -- instead of the quotient amax / 448.
@@ -68,9 +71,11 @@ __global__ __launch_bounds__(256) void quant_per_token_kernel(const uint16_t* __
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float sc = fmaxf(RECIP ? amax * (1.0f / kE4M3Max) : amax / kE4M3Max, eps);
-  if (threadIdx.x == 0) s[row] = sc;
+  if (threadIdx.x == 0 && blockIdx.y == 0) s[row] = sc;
   uint8_t* qr = q + row * K;
-  for (int i = threadIdx.x * 8; i < K; i += 256 * 8) {
+  const int chunk = ((K / 8 + gridDim.y - 1) / gridDim.y) * 8;
+  const int i0 = blockIdx.y * chunk, i1 = min(K, i0 + chunk);
+  for (int i = i0 + threadIdx.x * 8; i < i1; i += 256 * 8) {
     float f[8];
     load8<DT>(xr + i, f);
     float y[8];
@@ -425,8 +430,11 @@ static int quant_rows(const char* who, bool recip, const void* x, int x_dtype, i
   TI_CHECK_ARG(((uintptr_t)x & 15) == 0 && ((uintptr_t)xq & 7) == 0,
                "%s: input must be 16-byte and output 8-byte aligned", who);
   if (M == 0) return TI_OK;
-#define TI_QR(DT, R) \
-  hipLaunchKernelGGL((quant_per_token_kernel<DT, R>), dim3(M), dim3(256), 0, stream, (const uint16_t*)x, K, xq, xs, eps)
+  // column chunks: about 512 workgroups in all, each at least 2048 elements
+  const int chunks = std::max(1, std::min((511 + M) / M, K / 2048));
+#define TI_QR(DT, R)                                                                                             \
+  hipLaunchKernelGGL((quant_per_token_kernel<DT, R>), dim3(M, chunks), dim3(256), 0, stream, (const uint16_t*)x, K, \
+                     xq, xs, eps)
   if (x_dtype == TI_DTYPE_F16) {
     if (recip) TI_QR(TI_DTYPE_F16, true); else TI_QR(TI_DTYPE_F16, false);
   } else {
