@@ -27,6 +27,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only int4|fp8|moe]
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import statistics
@@ -387,7 +388,12 @@ def fp8_points(dev, stream):
                     recs.append(point_record(f"{label} incl. per-token quant {sname} M={m} K={k} N={n}", t,
                                              algo_q, flops, bound_q, FP8_PEAK_TFLOPS))
                     log(recs[-1])
-                    del x
+                    del x, launch_q
+                # Free this point's activations and outputs before the next point, so a
+                # large M's buffers do not stay allocated under the later points.
+                del a, asc, out, launch
+                gc.collect()
+                torch.cuda.empty_cache()
             del bq, bs
             torch.cuda.empty_cache()
     return recs
