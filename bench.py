@@ -335,6 +335,8 @@ def fp8_points(dev, stream):
             else:
                 bq = [torch.randint(-120, 120, (n, k), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
                       for _ in range(ncopy)]
+                if mode == 0:  # per-token FP8: the weights in the tiled layout the hooks cache
+                    bq = [_tiled_fp8_weight(b) for b in bq]
                 bs = [torch.rand((n,) if mode == 0 else (-(-n // 128), k // 128), device=dev) * 1e-3 + 1e-4
                       for _ in range(ncopy)]
             for m in ms:
@@ -348,8 +350,9 @@ def fp8_points(dev, stream):
                     j = i[0] % len(bq)
                     i[0] += 1
                     if mode == 0:
-                        r = L.ti_fp8_gemm_rowcol(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(),
-                                                 1, out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
+                        r = L.ti_fp8_gemm_rowcol_tiled(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(),
+                                                       bs[j].data_ptr(), 1, out.data_ptr(), 2, m, n, k,
+                                                       ws.data_ptr(), ws.numel() * 4, st)
                     elif mode == 2:
                         r = L.ti_fp4_gemm(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(), 1,
                                           out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
@@ -399,6 +402,14 @@ def fp8_points(dev, stream):
     return recs
 
 
+def _tiled_fp8_weight(w):
+    """Config 2's weights in the tiled layout the hooks cache (kernels.fp8.tile_weight_fp8,
+    prepared at load time, outside every timed region)."""
+    import torch
+    from torchinferno_amd.kernels import fp8 as tf8
+    return tf8.tile_weight_fp8(w.view(torch.float8_e4m3fn))
+
+
 def fp8_single_point(spec, launches, dev, stream):
     """Launch one config-2 (``rowcol:SHAPE:M``) or config-3 (``block:SHAPE:M``) GEMM
     `launches` times over rotating weight copies: the program a counter run profiles."""
@@ -411,6 +422,8 @@ def fp8_single_point(spec, launches, dev, stream):
     k, n = (FP8_SHAPES if mode == 0 else BLOCK_SHAPES)[sname]
     ncopy = max(2, -(-ROTATE_BYTES // (n * k)))
     bq = [torch.randint(-120, 120, (n, k), device=dev, dtype=torch.int8) for _ in range(ncopy)]
+    if mode == 0:
+        bq = [_tiled_fp8_weight(b) for b in bq]
     bs = [torch.rand((n,) if mode == 0 else (-(-n // 128), k // 128), device=dev) * 1e-3 + 1e-4
           for _ in range(ncopy)]
     a = torch.randint(-120, 120, (m, k), device=dev, dtype=torch.int8)
@@ -420,8 +433,8 @@ def fp8_single_point(spec, launches, dev, stream):
     for i in range(launches):
         j = i % ncopy
         if mode == 0:
-            r = L.ti_fp8_gemm_rowcol(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(), 1,
-                                     out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, stream)
+            r = L.ti_fp8_gemm_rowcol_tiled(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(),
+                                           1, out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, stream)
         else:
             r = L.ti_fp8_gemm_block(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(),
                                     out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, stream)

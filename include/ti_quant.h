@@ -225,6 +225,22 @@ int ti_fp8_gemm_rowcol(const uint8_t* a, const float* a_scale, int a_scale_per_r
                        void* out, int out_dtype, int M, int N, int K,
                        void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ti_fp8_gemm_rowcol with the weight in the tiled layout ti_fp8_tile_weight
+ * writes (N % 128 == 0).  No reference counterpart: the reference hands
+ * torch._scaled_mm the [N, K] weight; this build keeps its load-time FP8
+ * weight caches (the hooks' per-layer weight caches, tensor_parallel.py:
+ * 2958-2983) tiled, so that each 128-K step of a 128-row block is one
+ * contiguous 16 KiB run of HBM instead of 128 runs 128 bytes long. */
+int ti_fp8_gemm_rowcol_tiled(const uint8_t* a, const float* a_scale, int a_scale_per_row,
+                             const uint8_t* b_tiled, const float* b_scale, int b_scale_per_col,
+                             void* out, int out_dtype, int M, int N, int K,
+                             void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Re-lays an e4m3 weight w [N, K] (N, K % 128 == 0) as
+ * w_tiled[N/128][K/128][128][128]: block (n/128, k/128), row n % 128, byte
+ * k % 128.  N * K bytes; the weight format of ti_fp8_gemm_rowcol_tiled. */
+int ti_fp8_tile_weight(const uint8_t* w, int N, int K, uint8_t* w_tiled, hipStream_t stream);
+
 /* Block-scaled: out[m,n] = sum_kb (a . b^T over K block kb) * a_scale[m,kb] *
  * b_scale[n/128, kb]; b_scale [ceil(N/128), K/128] fp32; a_scale fp32
  * [M, K/128] for a_scale_layout 0 (the reference's), step-major [K/128, M]

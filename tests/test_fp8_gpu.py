@@ -466,3 +466,63 @@ def test_block_linear_3d_input(dev):
     assert y.shape == (2, 12, 256)
     xq, xs = tb.act_quant(x.view(24, 512))
     assert torch.equal(y.view(24, 256), tb.fp8_gemm(xq, xs, b, b_s))
+
+
+# --------------------------------------------------------------------------- tiled weights
+
+
+def test_tile_weight_layout(dev):
+    """ti_fp8_tile_weight: block (n // 128, k // 128), row n % 128, byte k % 128."""
+    from torchinferno_amd.kernels import fp8 as tf8
+    n, k = 384, 640
+    codes = torch.randint(0, 256, (n, k), dtype=torch.uint8, device=dev)
+    t = tf8.tile_weight_fp8(codes.view(torch.float8_e4m3fn))
+    assert t.shape == (n // 128, k // 128, 128, 128) and tf8.is_tiled_weight(t)
+    assert tf8.weight_nk(t) == (n, k)
+    c = codes.cpu().numpy()
+    expect = c.reshape(n // 128, 128, k // 128, 128).transpose(0, 2, 1, 3)
+    assert np.array_equal(t.view(torch.uint8).cpu().numpy(), expect)
+    with pytest.raises(ValueError):
+        tf8.tile_weight_fp8(codes[:200].view(torch.float8_e4m3fn))
+
+
+@pytest.mark.parametrize("m", [1, 16, 64, 200, 512])
+def test_tiled_weight_gemm_equals_row_layout(dev, m):
+    """The tiled weight gives the same bits as the [N, K] weight (same tiles, same
+    MFMA order), and the oracle's bound."""
+    from torchinferno_amd.kernels import fp8 as tf8
+    print(f"[fp8] tiled weight M={m}", flush=True)
+    x, xq, xs, wq, ws = _problem_rowcol(m, 1280, 640, 60 + m, dev)
+    wt = tf8.tile_weight_fp8(wq)
+    y = tf8.fp8_per_token_linear_quantized(xq, xs, wq, ws, out_dtype=torch.bfloat16)
+    yt = tf8.fp8_per_token_linear_quantized(xq, xs, wt, ws, out_dtype=torch.bfloat16)
+    assert torch.equal(y, yt)
+    assert torch.equal(tf8.fp8_per_token_linear(x, wt, ws), tf8.fp8_per_token_linear(x, wq, ws))
+    err = _check_rowcol(yt, xq, xs, wq, ws, np.random.default_rng(2))
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("kind", [k for k in range(18) if k not in (0, 7, 8)])
+def test_tiled_weight_every_kind(dev, monkeypatch, kind):
+    """Every 128-K-step tile kind (the 64-K-step kinds run kind 1 on tiled weights),
+    with and without split-K, on a ragged M: tiled equals row layout."""
+    from torchinferno_amd.kernels import fp8 as tf8
+    x, xq, xs, wq, ws = _problem_rowcol(200, 1280, 512, 80 + kind, dev)
+    wt = tf8.tile_weight_fp8(wq)
+    for splits in ("1", "3"):
+        monkeypatch.setenv("TI_ROCM_FP8_KIND", str(kind))
+        monkeypatch.setenv("TI_ROCM_FP8_SPLITS", splits)
+        y = tf8.fp8_per_token_linear_quantized(xq, xs, wq, ws, out_dtype=torch.bfloat16)
+        yt = tf8.fp8_per_token_linear_quantized(xq, xs, wt, ws, out_dtype=torch.bfloat16)
+        assert torch.equal(y, yt), (kind, splits)
+
+
+def test_prefill_linear_tiled_weight(dev):
+    from torchinferno_amd.kernels import fp8 as tf8
+    g = torch.Generator(device=dev).manual_seed(9)
+    w = (torch.randn((256, 512), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    x = torch.randn((40, 512), generator=g, device=dev).to(torch.bfloat16)
+    wq, sw = tf8.quantize_weight_fp8(w)
+    y = tf8.fp8_prefill_linear(x, wq, sw)
+    yt = tf8.fp8_prefill_linear(x, tf8.tile_weight_fp8(wq), sw)
+    assert torch.equal(y, yt)

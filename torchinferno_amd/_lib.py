@@ -55,6 +55,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ti_fp8_gemm_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "ti_fp8_gemm_workspace_bytes_max": (_sz, [_i, _i, _i, _i]),
     "ti_fp8_gemm_rowcol": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "ti_fp8_gemm_rowcol_tiled": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "ti_fp8_tile_weight": (_i, [_vp, _i, _i, _vp, _vp]),
     "ti_fp8_gemm_block": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ti_fp4_gemm": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ti_fp4_scale_stepmajor": (_i, [_vp, _i, _i, _vp, _vp]),

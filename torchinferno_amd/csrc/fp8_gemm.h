@@ -32,6 +32,7 @@ struct GemmArgs {
   long sb_expert_stride;    // 4-byte units between experts' weight-scale grids
   int sb_layout;            // SMODE 2: 0 = e8m0 [N, K/32]; 1 = step-major [K/128][N][4]
   int sa_layout;            // SMODE 1/2: 0 = [M, K/128]; 1 = step-major [K/128][M]
+  int b_tiled;              // 1: B in tiles of 128 rows x 128 K, [N/128][K/128][128][128] (e4m3)
 };
 
 struct GemmPlan {

@@ -219,9 +219,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
         row = min(n0 + r, N - 1);
       }
       dsrc[u] = is_a ? x.a + row * K + c * 16 : bmat + row * (F4 ? K / 2 : K) + c * 16;
+      dstep[u] = rowb;
+      if (SMODE == 0 && !is_a && x.b_tiled) {
+        // tiled weights (per-token / tensorwise mode only): each K step of 128 rows is one contiguous 16 KiB run
+        dsrc[u] = bmat + (row >> 7) * (128L * K) + (row & 127) * 128 + c * 16;
+        dstep[u] = 128 * 128;
+      }
       dlds[u] = (uint32_t)((is_a ? 0 : A_BYTES) + j * 1024);
       dwide[u] = true;
-      dstep[u] = rowb;
     } else if (id < NI_AB + NI_SA) {
       const int j = id - NI_AB;
       long row = min(m0 + min(j * 64 + lane, BM - 1), Mlim - 1);
@@ -861,7 +866,8 @@ using namespace ti::fp8;
 static int gemm_common(const char* name, int smode, const uint8_t* a, const float* a_scale,
                        int a_scale_stride, const uint8_t* b, const float* b_scale, int b_scale_stride,
                        void* out, int out_dtype, int M, int N, int K, void* workspace,
-                       size_t workspace_bytes, hipStream_t stream, int a_scale_layout = 0) {
+                       size_t workspace_bytes, hipStream_t stream, int a_scale_layout = 0,
+                       int b_tiled = 0) {
   TI_CHECK_ARG(a && b && a_scale && b_scale && out, "%s: null pointer", name);
   TI_CHECK_ARG(out_dtype == TI_DTYPE_BF16 || out_dtype == TI_DTYPE_F16, "%s: out dtype must be bf16 or fp16",
                name);
@@ -873,10 +879,12 @@ static int gemm_common(const char* name, int smode, const uint8_t* a, const floa
                "%s: misaligned out or scales", name);
   if (M == 0) return TI_OK;
   GemmPlan p = make_gemm_plan(M, N, K, smode);
+  if (b_tiled && (p.kind == 0 || p.kind == 7 || p.kind == 8)) p.kind = 1;  // tiles are 128-K steps
   GemmArgs x{};
   x.a = a; x.b = b; x.sa = a_scale; x.sb = b_scale;
   x.sa_stride = a_scale_stride; x.sb_stride = b_scale_stride;
   x.sb_layout = smode == 2 ? b_scale_stride : 0;
+  x.b_tiled = b_tiled;
   x.sa_layout = smode >= 1 ? a_scale_layout : 0;
   x.out = (uint16_t*)out;
   x.M = M; x.N = N; x.K = K;
@@ -921,6 +929,47 @@ extern "C" int ti_fp8_gemm_rowcol(const uint8_t* a, const float* a_scale, int a_
                                   hipStream_t stream) {
   return gemm_common("ti_fp8_gemm_rowcol", 0, a, a_scale, a_scale_per_row ? 1 : 0, b, b_scale,
                      b_scale_per_col ? 1 : 0, out, out_dtype, M, N, K, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ti_fp8_gemm_rowcol_tiled(const uint8_t* a, const float* a_scale, int a_scale_per_row,
+                                        const uint8_t* b_tiled, const float* b_scale, int b_scale_per_col,
+                                        void* out, int out_dtype, int M, int N, int K, void* workspace,
+                                        size_t workspace_bytes, hipStream_t stream) {
+  TI_CHECK_SHAPE(N % 128 == 0, "ti_fp8_gemm_rowcol_tiled: need N %% 128 == 0 (N=%d)", N);
+  return gemm_common("ti_fp8_gemm_rowcol_tiled", 0, a, a_scale, a_scale_per_row ? 1 : 0, b_tiled, b_scale,
+                     b_scale_per_col ? 1 : 0, out, out_dtype, M, N, K, workspace, workspace_bytes, stream, 0, 1);
+}
+
+namespace ti {
+namespace fp8 {
+namespace {
+
+// w [N, K] -> [N/128][K/128][128][128]: thread per 16-byte chunk of a row.
+__global__ __launch_bounds__(256) void tile_weight_kernel(const uint4* __restrict__ w, uint4* __restrict__ out,
+                                                          int N, int K) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;  // chunk index in [N, K/16]
+  const int cpr = K / 16;
+  if (i >= (long)N * cpr) return;
+  const int n = (int)(i / cpr), c = (int)(i % cpr);
+  const long dst = (((long)(n >> 7) * (K / 128) + (c >> 3)) * 128 + (n & 127)) * 8 + (c & 7);
+  out[dst] = w[i];
+}
+
+}  // namespace
+}  // namespace fp8
+}  // namespace ti
+
+extern "C" int ti_fp8_tile_weight(const uint8_t* w, int N, int K, uint8_t* w_tiled, hipStream_t stream) {
+  TI_CHECK_ARG(w && w_tiled, "ti_fp8_tile_weight: null pointer");
+  TI_CHECK_SHAPE(N > 0 && K > 0 && N % 128 == 0 && K % 128 == 0,
+                 "ti_fp8_tile_weight: need N %% 128 == 0 and K %% 128 == 0 (N=%d K=%d)", N, K);
+  TI_CHECK_ARG(((uintptr_t)w & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0,
+               "ti_fp8_tile_weight: w and w_tiled must be 16-byte aligned");
+  const long chunks = (long)N * (K / 16);
+  hipLaunchKernelGGL(ti::fp8::tile_weight_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream,
+                     (const uint4*)w, (uint4*)w_tiled, N, K);
+  TI_CHECK_LAUNCH("ti_fp8_tile_weight");
+  return TI_OK;
 }
 
 extern "C" int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, int a_scale_layout, const uint8_t* b,

@@ -155,6 +155,7 @@ def fp8_proj(self, hidden: Tensor, key: str, weight: Tensor, *, out: Tensor | No
                 setattr(self, f"_fp8_{key}_failed", True)
                 return None
             wq, sb = _fp8.quantize_weight_fp8(weight)
+            wq = _fp8.maybe_tile_weight_fp8(wq)  # the GEMM's tiled weight layout
             setattr(self, f"_fp8_{key}_wq", wq)
             setattr(self, f"_fp8_{key}_sb", sb)
         except Exception as exc:  # noqa: BLE001
@@ -198,6 +199,7 @@ def prepare_fp8_per_token_weight(self, key: str, weight: Tensor) -> tuple[Tensor
         return None
     try:
         wq, ws = _fp8.quantize_weight_fp8_per_channel(weight)
+        wq = _fp8.maybe_tile_weight_fp8(wq)  # the GEMM's tiled weight layout
         setattr(self, f"_fp8_per_token_{key}_wq", wq)
         setattr(self, f"_fp8_per_token_{key}_ws", ws)
         return wq, ws

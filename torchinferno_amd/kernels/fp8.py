@@ -10,8 +10,13 @@ returns ``None`` outside its supported region.  Every quantizer and GEMM runs on
 libti_quant.so's gfx950 kernels (``ti_fp8_*``); torch supplies only the tensorwise
 ``amax`` reduction and the reciprocal, as in the reference.
 
-Weights stay in the reference's ``[N, K]`` e4m3 layout (no repacking), so
-checkpoints and caches prepared for the reference load unchanged.
+The GEMMs take weights in the reference's ``[N, K]`` e4m3 layout, so checkpoints
+and caches prepared for the reference load unchanged, and also in this build's
+tiled layout (``tile_weight_fp8``: ``[N/128, K/128, 128, 128]``, each 128-K step
+of 128 rows one contiguous 16 KiB run), which the hooks' load-time weight caches
+use: measured 20-33% faster than ``[N, K]`` for the config-2 gate_up weight
+(470 MB) at decode M, where the row layout's 128-byte runs at an 8 KiB stride
+stream at 4.7 TB/s and the tiles at 5.9 TB/s.
 """
 from __future__ import annotations
 
@@ -151,6 +156,45 @@ def quantize_activation_fp8(
 # --------------------------------------------------------------------------- GEMMs
 
 
+def is_tiled_weight(w: Tensor) -> bool:
+    """A weight in the layout ``tile_weight_fp8`` writes."""
+    return w.ndim == 4 and w.dtype == FP8_E4M3 and w.size(2) == 128 and w.size(3) == 128
+
+
+def weight_nk(w: Tensor) -> tuple[int, int]:
+    """Logical ``(N, K)`` of an ``[N, K]`` or tiled e4m3 weight."""
+    if is_tiled_weight(w):
+        return w.size(0) * 128, w.size(1) * 128
+    return w.size(0), w.size(1)
+
+
+def tile_weight_fp8(weight_q: Tensor) -> Tensor:
+    """``[N, K]`` e4m3 weight -> ``[N/128, K/128, 128, 128]`` (N, K multiples of 128):
+    block (n // 128, k // 128), row n % 128, byte k % 128.  No reference counterpart."""
+    if weight_q.ndim != 2 or weight_q.dtype != FP8_E4M3:
+        raise ValueError("tile_weight_fp8 expects an [N, K] e4m3 weight")
+    n, k = weight_q.shape
+    if n % 128 or k % 128:
+        raise ValueError("tile_weight_fp8 needs N and K multiples of 128")
+    _lib.require_device(weight_q)
+    src = weight_q.contiguous()
+    out = torch.empty((n // 128, k // 128, 128, 128), dtype=FP8_E4M3, device=weight_q.device)
+    _lib.call("ti_fp8_tile_weight", src.data_ptr(), n, k, out.data_ptr(), _lib.stream_of(src))
+    return out
+
+
+def maybe_tile_weight_fp8(weight_q: Tensor) -> Tensor:
+    """The tiled form when the shape allows it (and ``TI_ROCM_FP8_TILED_WEIGHTS`` is
+    not ``0``), else the weight unchanged."""
+    import os
+    if os.environ.get("TI_ROCM_FP8_TILED_WEIGHTS", "1") == "0":
+        return weight_q
+    if (weight_q.ndim == 2 and weight_q.dtype == FP8_E4M3 and weight_q.size(0) % 128 == 0
+            and weight_q.size(1) % 128 == 0 and weight_q.is_cuda):
+        return tile_weight_fp8(weight_q)
+    return weight_q
+
+
 def _pad_k(t: Tensor, k_pad: int) -> Tensor:
     out = torch.zeros((t.size(0), k_pad), dtype=t.dtype, device=t.device)
     out[:, : t.size(1)] = t
@@ -160,7 +204,16 @@ def _pad_k(t: Tensor, k_pad: int) -> Tensor:
 def _gemm_rowcol(a: Tensor, a_scale: Tensor, b_nk: Tensor, b_scale: Tensor, out: Tensor) -> None:
     """out[M,N] = (a . b_nk^T) * a_scale * b_scale on the ti kernel.  The kernel walks
     K in 128-byte steps; other K (the reference accepts K % 16 == 0) are zero-padded
-    here -- zero codes add exact zeros, so the result is unchanged."""
+    here -- zero codes add exact zeros, so the result is unchanged.  A tiled ``b_nk``
+    (``tile_weight_fp8``) runs ``ti_fp8_gemm_rowcol_tiled``."""
+    if is_tiled_weight(b_nk):
+        m, k = a.shape
+        n = b_nk.size(0) * 128
+        ws, ws_bytes = _ws_args(a.device, m, n, k, 0)
+        _lib.call("ti_fp8_gemm_rowcol_tiled", a.data_ptr(), a_scale.data_ptr(), int(a_scale.numel() != 1),
+                  b_nk.data_ptr(), b_scale.data_ptr(), int(b_scale.numel() != 1), out.data_ptr(),
+                  _lib.dtype_code(out.dtype), m, n, k, ws, ws_bytes, _lib.stream_of(a))
+        return
     if a.size(1) % K_ALIGN:
         k_pad = -(-a.size(1) // K_ALIGN) * K_ALIGN
         a, b_nk = _pad_k(a, k_pad), _pad_k(b_nk, k_pad)
@@ -182,14 +235,14 @@ def fp8_prefill_linear(
 ) -> Tensor:
     """``x @ weight.t()`` with tensorwise FP8 scales (fp8.py:184-205): dynamic (or
     static) tensorwise activation quant, then the W8A8 GEMM; returns bf16."""
-    k = wq.size(1)
+    n, k = weight_nk(wq)
     x2d = x.reshape(-1, k)
     xq, sa = quantize_activation_fp8(x2d, scale=activation_scale,
                                      inverse_scale=activation_inverse_scale)
-    out = torch.empty((x2d.size(0), wq.size(0)), dtype=torch.bfloat16, device=x.device)
+    out = torch.empty((x2d.size(0), n), dtype=torch.bfloat16, device=x.device)
     _gemm_rowcol(xq, sa.reshape(1).contiguous(), wq.contiguous(),
                  weight_scale.to(torch.float32).reshape(1).contiguous(), out)
-    return out.reshape(*x.shape[:-1], wq.size(0))
+    return out.reshape(*x.shape[:-1], n)
 
 
 def fp8_per_token_linear(
@@ -201,13 +254,14 @@ def fp8_per_token_linear(
     use_fast_accum: bool = False,
 ) -> Tensor:
     """W8A8 with dynamic per-token and per-channel scales (fp8.py:208-247)."""
-    if x.ndim < 2 or weight_q.ndim != 2:
+    if x.ndim < 2 or (weight_q.ndim != 2 and not is_tiled_weight(weight_q)):
         raise ValueError("FP8 linear expects an activation matrix and [N, K] weight")
     if weight_q.dtype != FP8_E4M3 or weight_q.device != x.device:
         raise ValueError("FP8 weight must use e4m3 on the activation device")
-    if weight_q.size(1) != x.size(-1):
+    n, k = weight_nk(weight_q)
+    if k != x.size(-1):
         raise ValueError("FP8 activation and weight inner dimensions must match")
-    if weight_scale.shape != (1, weight_q.size(0)) or weight_scale.device != x.device:
+    if weight_scale.shape != (1, n) or weight_scale.device != x.device:
         raise ValueError("per-channel FP8 weight scale must have shape [1, N]")
     x_q, x_scale = quantize_activation_fp8_per_token(x)
     return fp8_per_token_linear_quantized(
@@ -236,19 +290,19 @@ def fp8_per_token_linear_quantized(
     accumulates in fp32 (there is no reduced-precision accumulation mode)."""
     if x_q.ndim < 2 or x_q.dtype != FP8_E4M3:
         raise ValueError("quantized FP8 activation must be an e4m3 matrix")
-    if weight_q.ndim != 2 or weight_q.dtype != FP8_E4M3:
+    if (weight_q.ndim != 2 and not is_tiled_weight(weight_q)) or weight_q.dtype != FP8_E4M3:
         raise ValueError("FP8 weight must be an e4m3 matrix")
-    if x_q.device != weight_q.device or x_q.size(-1) != weight_q.size(1):
+    n, k = weight_nk(weight_q)
+    if x_q.device != weight_q.device or x_q.size(-1) != k:
         raise ValueError("FP8 activation and weight must have matching devices and inner dimensions")
     rows = x_q.numel() // x_q.size(-1)
     if x_scale.shape != (rows, 1) or x_scale.device != x_q.device:
         raise ValueError("per-token FP8 activation scale must have shape [rows, 1]")
-    if weight_scale.shape != (1, weight_q.size(0)) or weight_scale.device != x_q.device:
+    if weight_scale.shape != (1, n) or weight_scale.device != x_q.device:
         raise ValueError("per-channel FP8 weight scale must have shape [1, N]")
     if out_dtype not in _OUT_DTYPES:
         raise ValueError("FP8 linear output dtype must be bf16 or fp16")
     _lib.require_device(x_q)
-    n = weight_q.size(0)
     expected_shape = (*x_q.shape[:-1], n)
     if out is not None:
         if tuple(out.shape) != expected_shape or out.device != x_q.device or out.dtype != out_dtype:

@@ -83,7 +83,7 @@ def fp8_per_token_linear(x: Tensor, weight_q: Tensor, weight_scale: Tensor) -> T
 
 @fp8_per_token_linear.register_fake
 def _fp8_per_token_linear_fake(x, weight_q, weight_scale):
-    return x.new_empty((*x.shape[:-1], weight_q.size(0)))
+    return x.new_empty((*x.shape[:-1], fp8.weight_nk(weight_q)[0]))
 
 
 @torch.library.custom_op(f"{_NS}::act_quant", mutates_args=())
