@@ -729,9 +729,10 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   // tiles -- 128 with block or MXFP4 scales -- then 128x128).
   auto tiles = [&](int bm, int bn) { return (long)cdiv(M, bm) * cdiv(N, bn); };
   int splits = 1;
-  if (M <= 4) {
-    // Split over K below 128 column tiles: up to 4 ways, 8 at deep K (down
-    // M=1, K=28672: 51.7 -> 44.1 us).
+  if (M <= 4 && (smode != 0 || tiles(16, 256) >= 128)) {
+    // 4-wave 16x256 tiles; split over K below 128 column tiles: up to 4 ways,
+    // 8 at deep K.  (Per-token FP8 below 128 such tiles takes the 8-wave 16x128
+    // split below instead: config-2 qkv M=1 17 -> 16 us, down M=1 46 -> 43 us.)
     p.kind = 3;
     const long t = tiles(16, 256);
     const int cap = K >= 16384 ? 8 : 4;
