@@ -83,6 +83,10 @@ def test_fp8_proj_tensorwise_and_per_token(dev, layer, monkeypatch):
     ref = x.float() @ w.float().t()
     torch.testing.assert_close(y.float(), ref, atol=1.0, rtol=0.15)
     assert layer._fp8_gu_wq.dtype == torch.float8_e4m3fn
+    from torchinferno_amd.kernels import fp8 as tf8
+    assert tf8.is_tiled_weight(layer._fp8_gu_wq)  # the cache holds the GEMM's tiled layout
+    wq_rows, sb_rows = tf8.quantize_weight_fp8(w)
+    assert torch.equal(y, tf8.fp8_prefill_linear(x, wq_rows, sb_rows))  # same bits as [N, K]
     assert layer._fp8_proj(x[:200], "gu", w) is None  # M <= 256 gate
     monkeypatch.setenv("TORCHINFERNO_FP8_PER_TOKEN_SCALE", "1")
     out = torch.empty((300, 512), dtype=torch.bfloat16, device=dev)
