@@ -317,17 +317,22 @@ def point_record(label, t_s, algo_bytes, flops, bound, peak_tf, extra=None):
 
 def fp8_points(dev, stream):
     """Config 2 (rowcol) and config 3 (block) GEMMs on pre-quantized activations, and
-    config 2 at M=64 and 4096 again with the per-token activation quant timed in."""
+    config 2 at M=64 and 4096 again with the per-token activation quant timed in.
+    Modes 3 and 4 time config 3's shapes with DeepSeek-V4's power-of-two (ue8m0 /
+    E8M0) scales, which the MFMA applies (block FP8 and MXFP4)."""
     import torch
     from torchinferno_amd import _lib
     L = _lib.lib()
     ws = torch.zeros(64 << 20, dtype=torch.int32, device=dev)
     recs = []
-    for mode, shapes, ms in ((0, FP8_SHAPES, FP8_MS), (1, BLOCK_SHAPES, BLOCK_MS), (2, BLOCK_SHAPES, BLOCK_MS)):
+    for mode, shapes, ms in ((0, FP8_SHAPES, FP8_MS), (1, BLOCK_SHAPES, BLOCK_MS), (2, BLOCK_SHAPES, BLOCK_MS),
+                             (3, BLOCK_SHAPES, BLOCK_MS), (4, BLOCK_SHAPES, BLOCK_MS)):
+        f4 = mode in (2, 4)
+        pow2 = mode >= 3
         for sname, (k, n) in shapes.items():
-            wbytes_n = n * k // 2 if mode == 2 else n * k
+            wbytes_n = n * k // 2 if f4 else n * k
             ncopy = max(2, -(-ROTATE_BYTES // wbytes_n))
-            if mode == 2:  # MXFP4: e2m1 pairs, e8m0 scale per 32 K
+            if f4:  # MXFP4: e2m1 pairs, e8m0 scale per 32 K
                 bq = [torch.randint(0, 256, (n, k // 2), device=dev, dtype=torch.uint8) for _ in range(ncopy)]
                 from torchinferno_amd.kernels.block_fp8 import fp4_scale_stepmajor
                 bs = [fp4_scale_stepmajor(torch.randint(118, 130, (n, k // 32), device=dev, dtype=torch.uint8))
@@ -339,10 +344,14 @@ def fp8_points(dev, stream):
                     bq = [_tiled_fp8_weight(b) for b in bq]
                 bs = [torch.rand((n,) if mode == 0 else (-(-n // 128), k // 128), device=dev) * 1e-3 + 1e-4
                       for _ in range(ncopy)]
+                if pow2:
+                    bs = [torch.exp2(torch.randint(-13, -9, b.shape, device=dev).float()) for b in bs]
             for m in ms:
                 a = torch.randint(-120, 120, (m, k), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
-                # modes 1/2: step-major activation scales [K/128, M], as the DSv4 linear path keeps them
+                # modes 1-4: step-major activation scales [K/128, M], as the DSv4 linear path keeps them
                 asc = torch.rand((m,) if mode == 0 else (k // 128, m), device=dev) * 0.01 + 1e-3
+                if pow2:
+                    asc = torch.exp2(torch.randint(-10, -6, asc.shape, device=dev).float())
                 out = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
                 i = [0]
 
@@ -353,23 +362,26 @@ def fp8_points(dev, stream):
                         r = L.ti_fp8_gemm_rowcol_tiled(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(),
                                                        bs[j].data_ptr(), 1, out.data_ptr(), 2, m, n, k,
                                                        ws.data_ptr(), ws.numel() * 4, st)
-                    elif mode == 2:
-                        r = L.ti_fp4_gemm(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(), 1,
-                                          out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
+                    elif mode in (2, 4):
+                        fn = L.ti_fp4_gemm_pow2 if mode == 4 else L.ti_fp4_gemm
+                        r = fn(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(), 1,
+                               out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
                     else:
-                        r = L.ti_fp8_gemm_block(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(),
-                                                out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
+                        fn = L.ti_fp8_gemm_block_pow2 if mode == 3 else L.ti_fp8_gemm_block
+                        r = fn(a.data_ptr(), asc.data_ptr(), 1, bq[j].data_ptr(), bs[j].data_ptr(),
+                               out.data_ptr(), 2, m, n, k, ws.data_ptr(), ws.numel() * 4, st)
                     _check("fp8 gemm", r)
 
                 reps = 10 if m >= 4096 else 40
                 timed_burst([launch], 3, stream)
                 t = timed_burst([launch], reps, stream) / reps * 1e-3
                 flops = 2 * m * n * k
-                scale_bytes = (n * 4 if mode == 0 else (-(-n // 128)) * (k // 128) * 4 if mode == 1
+                scale_bytes = (n * 4 if mode == 0 else (-(-n // 128)) * (k // 128) * 4 if mode in (1, 3)
                                else n * (k // 32))
                 algo = wbytes_n + scale_bytes + m * k + m * n * 2
                 bound = "mfma" if flops / algo > FP8_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
-                label = {0: "config2 fp8 rowcol", 1: "config3 fp8 block", 2: "config3-shape mxfp4"}[mode]
+                label = {0: "config2 fp8 rowcol", 1: "config3 fp8 block", 2: "config3-shape mxfp4",
+                         3: "config3-shape fp8 block ue8m0", 4: "config3-shape mxfp4 ue8m0"}[mode]
                 recs.append(point_record(f"{label} {sname} M={m} K={k} N={n}", t, algo, flops, bound,
                                          FP8_PEAK_TFLOPS))
                 log(recs[-1])
@@ -533,6 +545,11 @@ def moe_points(dev, stream):
     recs = []
     per_expert = 2 * inter * h + h * inter + (s13[0].numel() + s2[0].numel()) * 4
     recs += _moe_sweep(L, dev, "config4 fp8 moe", "ti_fp8_moe", w13, s13, w2, s2, e, h, inter, k, per_expert)
+    # DeepSeek-V4's scale format: ue8m0 activations and E8M0 weight scales, applied by the MFMA
+    s13, s2 = torch.exp2(torch.randint(-13, -9, s13.shape, device=dev).float()), \
+        torch.exp2(torch.randint(-13, -9, s2.shape, device=dev).float())
+    recs += _moe_sweep(L, dev, "config4-shape fp8 moe ue8m0", "ti_fp8_moe", w13, s13, w2, s2, e, h, inter, k,
+                       per_expert, round_scale=2)
     del w13, w2, s13, s2
     torch.cuda.empty_cache()
     # The same routed experts with MXFP4 weights (e2m1 pairs, e8m0 per 32 K).
@@ -544,12 +561,14 @@ def moe_points(dev, stream):
     per_expert = (2 * inter * h + h * inter) // 2 + s13[0].numel() + s2[0].numel()
     recs += _moe_sweep(L, dev, "config4-shape mxfp4 moe", "ti_fp4_moe", w13, s13, w2, s2, e, h, inter, k,
                        per_expert)
+    recs += _moe_sweep(L, dev, "config4-shape mxfp4 moe ue8m0", "ti_fp4_moe", w13, s13, w2, s2, e, h, inter, k,
+                       per_expert, round_scale=2)
     del w13, w2
     torch.cuda.empty_cache()
     return recs
 
 
-def _moe_sweep(L, dev, label, entry, w13, s13, w2, s2, e, h, inter, k, per_expert):
+def _moe_sweep(L, dev, label, entry, w13, s13, w2, s2, e, h, inter, k, per_expert, round_scale=0):
     import torch
     stream = torch.cuda.current_stream(dev).cuda_stream
     fn = getattr(L, entry)
@@ -569,7 +588,7 @@ def _moe_sweep(L, dev, label, entry, w13, s13, w2, s2, e, h, inter, k, per_exper
             _check("route", L.ti_moe_route_topk(logits.data_ptr(), t, e, k, 1, 1.0, wts.data_ptr(), ids.data_ptr(), st))
             lay = (1,) if entry == "ti_fp4_moe" else ()
             _check("moe", fn(x.data_ptr(), wts.data_ptr(), ids.data_ptr(), t, k, w13.data_ptr(),
-                             s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), *lay, e, h, inter, 0.0, 0,
+                             s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), *lay, e, h, inter, 0.0, round_scale,
                              out.data_ptr(), wsp, need, st))
 
         timed_burst([launch], 2, stream)

@@ -209,7 +209,9 @@ int ti_fp8_swiglu_quant_per_token(const void* gate, long gate_row_stride, const 
  * ti_fp8_gemm_workspace_bytes() (zero-filled once when allocated; every call
  * leaves its ticket words zero again; calls sharing one workspace must be
  * stream-ordered).  scale_mode: 0 = row/column scales, 1 = 128x128 blocks,
- * 2 = MXFP4 weights (ti_fp4_gemm).
+ * 2 = MXFP4 weights (ti_fp4_gemm), 3 = power-of-two 128x128 blocks
+ * (ti_fp8_gemm_block_pow2), 4 = MXFP4 with power-of-two activation scales
+ * (ti_fp4_gemm_pow2).
  * ------------------------------------------------------------------------- */
 size_t ti_fp8_gemm_workspace_bytes(int M, int N, int K, int scale_mode);
 size_t ti_fp8_gemm_workspace_bytes_max(int max_m, int N, int K, int scale_mode);
@@ -265,6 +267,24 @@ int ti_fp4_gemm(const uint8_t* a, const float* a_scale, int a_scale_layout, cons
                 const uint8_t* b_scale, int b_scale_layout, void* out, int out_dtype, int M, int N, int K, void* workspace,
                 size_t workspace_bytes, hipStream_t stream);
 
+/* ti_fp8_gemm_block and ti_fp4_gemm for DeepSeek-V4's "ue8m0" scale format:
+ * every a_scale (and, for the block GEMM, every b_scale) value is a power of
+ * two in the E8M0 range, 2^-127 .. 2^127, stored as fp32 -- the scales
+ * act_quant writes with a scale_fmt and the float8_e8m0fnu weight scales of
+ * the reference's scale_dtype=float8_e8m0fnu path (deepseek_v4_tilelang.py:
+ * 207-223, tensor_parallel.py:1211-1212).  The MFMA applies the scales as
+ * exponents (gfx950 block-scaled f8f6f4), so the per-128-K fold of the fp32
+ * paths disappears; the result is the same sum, differing only in fp32
+ * accumulation order.  Only the exponent field of each scale is read: other
+ * values are not rejected but give wrong results.  Same arguments, layouts
+ * and workspace (scale_mode 3 and 4) as the fp32-scale entry points. */
+int ti_fp8_gemm_block_pow2(const uint8_t* a, const float* a_scale, int a_scale_layout, const uint8_t* b,
+                           const float* b_scale, void* out, int out_dtype, int M, int N, int K,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream);
+int ti_fp4_gemm_pow2(const uint8_t* a, const float* a_scale, int a_scale_layout, const uint8_t* b,
+                     const uint8_t* b_scale, int b_scale_layout, void* out, int out_dtype, int M, int N, int K,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* E8M0 scales [N, K/32] -> step-major [K/128][N][4] (weight preparation, run
  * once per weight; no counterpart in the reference, whose kernels read the
  * checkpoint layout). */
@@ -300,7 +320,9 @@ size_t ti_fp8_moe_workspace_bytes(int T, int k, int E, int H, int I);
  *   clamp_limit > 0 clamps gate <= limit and |up| <= limit (swiglu_limit);
  *   round_scale != 0 gives both activation quants power-of-two scales
  *   (act_quant with scale_fmt "ue8m0", the DSv4 checkpoint setting,
- *   tensor_parallel.py:195-207,1199-1211);
+ *   tensor_parallel.py:195-207,1199-1211); round_scale 2 also declares every
+ *   s13 / s2 value a power of two (E8M0 weight scales), and the grouped GEMMs
+ *   then apply all scales inside the MFMA, as ti_fp8_gemm_block_pow2;
  *   out bf16 [T,H].  H, I multiples of 128.  Deterministic. */
 int ti_fp8_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids,
                int T, int k, const uint8_t* w13, const float* s13, const uint8_t* w2,
@@ -314,7 +336,9 @@ int ti_fp8_moe(const void* hidden, const float* topk_weights, const int32_t* top
  * 195-207).  Replaces fused_mxfp4_moe (deepseek_v4_marlin.py:311-411).
  *   w13 e2m1 [E, 2I, H/2], s13 E8M0 per expert [2I, H/32] (scale_layout 0) or
  *   step-major [H/128][2I][4] (scale_layout 1); w2 e2m1 [E, H, I/2], s2 per
- *   expert [H, I/32] or [I/128][H][4]; workspace as ti_fp8_moe_workspace_bytes. */
+ *   expert [H, I/32] or [I/128][H][4]; workspace as ti_fp8_moe_workspace_bytes.
+ *   round_scale 2: as 1, with the power-of-two activation scales applied
+ *   inside the MFMA next to the weight's, as ti_fp4_gemm_pow2. */
 int ti_fp4_moe(const void* hidden, const float* topk_weights, const int32_t* topk_ids,
                int T, int k, const uint8_t* w13, const uint8_t* s13, const uint8_t* w2,
                const uint8_t* s2, int scale_layout, int E, int H, int I, float clamp_limit,

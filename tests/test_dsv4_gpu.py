@@ -117,8 +117,9 @@ def test_linear_ue8m0_fp4_matches_oracle(dev, m, k, n):
 
 
 def test_block_api_e8m0_scale_storage(dev):
-    """act_quant(scale_dtype=float8_e8m0fnu) returns the same powers of two as E8M0, and
-    fp8_gemm on E8M0 scales equals fp8_gemm on their fp32 values bit for bit."""
+    """act_quant(scale_dtype=float8_e8m0fnu) returns the same powers of two as E8M0;
+    fp8_gemm on E8M0 scales equals the power-of-two GEMM on their fp32 values bit for
+    bit, and both it and the fp32-scale GEMM are within the oracle's bound."""
     from torchinferno_amd.kernels import block_fp8 as tb
     rng = np.random.default_rng(3)
     wt, codes, s = _fp8_weight(256, 1024, rng, dev, torch.float8_e8m0fnu)
@@ -129,7 +130,12 @@ def test_block_api_e8m0_scale_storage(dev):
     assert torch.equal(q8.view(torch.uint8), q32.view(torch.uint8))
     y8 = tb.fp8_gemm(q8, s8, wt, wt.scale, torch.float8_e8m0fnu)
     y32 = tb.fp8_gemm(q32, s32, wt, wt.scale.float())
-    assert torch.equal(y8, y32)
+    assert torch.equal(y8, tb._fp8_gemm_raw(q32, s32, 0, wt, wt.scale.float(), True))
+    xq, xs = _codes(q32), s32.cpu().numpy()
+    ref = ofp8.fp8_gemm_block(xq, xs, codes, s)
+    ref_abs = ofp8.fp8_gemm_block(abs_codes(xq), xs, abs_codes(codes), s)
+    for y in (y8, y32):
+        assert elementwise_ratio(y.float().cpu().numpy(), ref, ref_abs) <= 1.0
     with pytest.raises(ValueError):
         tb.act_quant(x, 128, None, torch.float8_e8m0fnu)
     with pytest.raises(ValueError):
@@ -144,6 +150,8 @@ def _moe_model(mod, e, h, inter, k, fmt, clamp, rng, dev):
     def weight(n, kk):
         if fmt == "fp8":
             return _fp8_weight(n, kk, rng, dev, torch.float32)[0]
+        if fmt == "fp8e8m0":  # E8M0 weight scales: all scales powers of two
+            return _fp8_weight(n, kk, rng, dev, torch.float8_e8m0fnu)[0]
         return _fp4_weight(n, kk, rng, dev)[0]
 
     class Lin:
@@ -181,19 +189,20 @@ def _host_experts(m, fmt):
     for ex in m.experts:
         w13 = np.concatenate([_codes(ex.w1.weight), _codes(ex.w3.weight)])
         w2 = _codes(ex.w2.weight)
-        s13 = np.concatenate([_codes(ex.w1.scale) if fmt == "fp4" else ex.w1.scale.cpu().numpy(),
-                              _codes(ex.w3.scale) if fmt == "fp4" else ex.w3.scale.cpu().numpy()])
-        s2 = _codes(ex.w2.scale) if fmt == "fp4" else ex.w2.scale.cpu().numpy()
+        s13 = np.concatenate([_codes(ex.w1.scale) if fmt == "fp4" else ex.w1.scale.float().cpu().numpy(),
+                              _codes(ex.w3.scale) if fmt == "fp4" else ex.w3.scale.float().cpu().numpy()])
+        s2 = _codes(ex.w2.scale) if fmt == "fp4" else ex.w2.scale.float().cpu().numpy()
         out.append((w13, s13, w2, s2))
     return out
 
 
-@pytest.mark.parametrize("fmt", ["fp8", "fp4"])
+@pytest.mark.parametrize("fmt", ["fp8", "fp8e8m0", "fp4"])
 @pytest.mark.parametrize("t,clamp", [(5, 0.0), (40, 0.0), (300, 0.4)])
 def test_moe_hook_ue8m0_matches_oracle(dev, fmt, t, clamp):
     """MoE.forward with fused experts (prepare_fused_experts -> fused_{fp8,mxfp4}_moe)
     under scale_fmt "ue8m0": every expert Linear quantizes its input with power-of-two
-    scales, as the reference's Expert -> linear -> act_quant does."""
+    scales, as the reference's Expert -> linear -> act_quant does.  With E8M0 weight
+    scales (fp8e8m0, fp4) the grouped GEMMs apply all scales inside the MFMA."""
     from torchinferno_amd import hooks
     print(f"[dsv4] moe hook {fmt} ue8m0 T={t} clamp={clamp}", flush=True)
     mod, undo = _fake_module(f"fake_dsv4_moe_{fmt}_{t}", "ue8m0", torch.float32)
@@ -205,7 +214,7 @@ def test_moe_hook_ue8m0_matches_oracle(dev, fmt, t, clamp):
         x = torch.from_numpy(rng.standard_normal((t, h)).astype(np.float32)).to(torch.bfloat16).to(dev)
         y = hooks.moe_forward(m, x.view(1, t, h), torch.zeros((1, t), dtype=torch.long, device=dev))
         w, ids = m.gate(x, None)
-        lin = omoe.block_fp8_linear if fmt == "fp8" else omoe.mxfp4_linear
+        lin = omoe.mxfp4_linear if fmt == "fp4" else omoe.block_fp8_linear
         args = (x.float().cpu().numpy(), w.cpu().numpy(), ids.cpu().numpy(), _host_experts(m, fmt))
         ref = omoe.moe_reference(*args, linear=omoe.ue8m0(lin), clamp_limit=clamp)
         got = y.view(t, h).float().cpu().numpy()

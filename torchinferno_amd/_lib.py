@@ -59,6 +59,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ti_fp8_tile_weight": (_i, [_vp, _i, _i, _vp, _vp]),
     "ti_fp8_gemm_block": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ti_fp4_gemm": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "ti_fp8_gemm_block_pow2": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "ti_fp4_gemm_pow2": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ti_fp4_scale_stepmajor": (_i, [_vp, _i, _i, _vp, _vp]),
     "ti_moe_route_topk": (_i, [_vp, _i, _i, _i, _i, _f, _vp, _vp, _vp]),
     "ti_fp8_moe_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),

@@ -10,7 +10,12 @@
 //   * MXFP4 weights (SMODE 2): B is e2m1, two per byte along K, with one E8M0
 //     scale per 32 K of a row, applied by the MFMA itself (its per-lane block
 //     scale operand); A keeps its 1x128 fp32 scales, folded per K step --
-//     DeepSeek fp4_gemm, deepseek_v4_tilelang_definitions.py:674-769.
+//     DeepSeek fp4_gemm, deepseek_v4_tilelang_definitions.py:674-769;
+//   * power-of-two block scales (SMODE 3: block FP8; SMODE 4: MXFP4 with
+//     power-of-two activation scales) -- DeepSeek-V4's ue8m0 format
+//     (scale_dtype float8_e8m0fnu, deepseek_v4_tilelang.py:207-223): every
+//     scale is an exponent, so the MFMA's per-lane E8M0 scale operands apply
+//     both of them and the partial sums accumulate in the MFMA with no fold.
 // A (and B outside SMODE 2) are K-contiguous e4m3 (OCP float8_e4m3fn,
 // gfx950's native FP8).
 //
@@ -57,6 +62,14 @@ struct Mfma<32> {
   static __device__ __forceinline__ acc_t mma4(i32x8 a, i32x8 b, acc_t c, int eb) {
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 4, 0, 127, 0, eb);
   }
+  // E8M0 scales ea (A row of this lane) and eb (B row of this lane), each
+  // covering the lane's 32 K values.
+  static __device__ __forceinline__ acc_t mma_s(i32x8 a, i32x8 b, acc_t c, int ea, int eb) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, ea, 0, eb);
+  }
+  static __device__ __forceinline__ acc_t mma4_s(i32x8 a, i32x8 b, acc_t c, int ea, int eb) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 4, 0, ea, 0, eb);
+  }
   // Row (within the 32x32 tile) of accumulator element e of this lane.
   static __device__ __forceinline__ int row(int e, int lane) { return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3); }
   // First of the two 16-byte chunks (of the 128-byte K step) lane reads for MFMA ks.
@@ -84,6 +97,12 @@ struct Mfma<16> {
   static __device__ __forceinline__ acc_t mma4(i32x8 a, i32x8 b, acc_t c, int eb) {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 4, 0, 127, 0, eb);
   }
+  static __device__ __forceinline__ acc_t mma_s(i32x8 a, i32x8 b, acc_t c, int ea, int eb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, ea, 0, eb);
+  }
+  static __device__ __forceinline__ acc_t mma4_s(i32x8 a, i32x8 b, acc_t c, int ea, int eb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 4, 0, ea, 0, eb);
+  }
   static __device__ __forceinline__ int row(int e, int lane) { return 4 * (lane >> 4) + e; }
   static __device__ __forceinline__ int chunk(int, int lane) { return (lane >> 4) * 2; }
   static __device__ __forceinline__ int chunk4(int, int lane) { return lane >> 4; }
@@ -103,6 +122,10 @@ __device__ __forceinline__ int swz(int r, int c) {
   return (r * CPR + (c ^ ((r / RP) % CPR))) * 16;
 }
 
+// E8M0 byte of a power-of-two fp32 scale: its exponent field (2^-127, the
+// subnormal 0x00400000, gives 0 as well).
+__device__ __forceinline__ int e8m0_of(float s) { return (int)((__float_as_uint(s) >> 23) & 0xFFu); }
+
 template <int ODT>
 __device__ __forceinline__ uint16_t out_bits(float v) {
   if constexpr (ODT == TI_DTYPE_F16) return f32_to_f16_bits(v);
@@ -117,10 +140,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
   constexpr int TM = BM / WGM, TN = BN / WGN;
   constexpr int FM = TM / MF, FN = TN / MF;
   static_assert(FM >= 1 && FN >= 1 && TM % MF == 0 && TN % MF == 0, "wave tile must hold whole MFMA tiles");
-  static_assert(SMODE != 1 || 128 % TN == 0, "block scales need a wave's columns inside one 128 block");
+  constexpr bool BLK = SMODE == 1 || SMODE == 3;  // 128x128 block weight scales
+  constexpr bool F4 = SMODE == 2 || SMODE == 4;   // e2m1 B with E8M0 scales per 32 K
+  constexpr bool PW2 = SMODE >= 3;                // all scales powers of two, applied by the MFMA
+  static_assert(!BLK || 128 % TN == 0, "block scales need a wave's columns inside one 128 block");
   static_assert(BK == 128 || (BK == 64 && MF == 32), "16x16x128 MFMAs need 128-byte K steps");
-  static_assert(SMODE != 2 || BK == 128, "e2m1 B takes 128-wide K steps (64-byte rows)");
-  constexpr bool F4 = SMODE == 2;
+  static_assert(!F4 || BK == 128, "e2m1 B takes 128-wide K steps (64-byte rows)");
   constexpr int BROW = F4 ? BK / 2 : BK;           // B bytes per row per K step
   constexpr int KS = BK / (MF == 32 ? 64 : 128);  // MFMAs per K step
   constexpr int CPR = BK / 16;                     // 16-byte chunks per row
@@ -130,7 +155,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
   // mode then the weight scales of the tile's 128-column blocks (one 256-byte
   // DMA), MXFP4 mode the BN rows' four e8m0 bytes of the step (one dword each).
   constexpr int SA_ROWS = SMODE >= 1 ? ((BM * 4 + 255) / 256) * 256 : 0;
-  constexpr int SB_BYTES = SMODE == 1 ? 256 : (SMODE == 2 ? ((BN * 4 + 255) / 256) * 256 : 0);
+  constexpr int SB_BYTES = BLK ? 256 : (F4 ? ((BN * 4 + 255) / 256) * 256 : 0);
   constexpr int SA_BYTES = SA_ROWS + SB_BYTES;
   constexpr int STAGE = A_BYTES + B_BYTES + SA_BYTES;
   constexpr int NI_AB = (A_BYTES + B_BYTES) / 1024;
@@ -238,7 +263,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
       dwide[u] = false;
       dstep[u] = x.sa_layout ? M * 4 : 4;
       dper128[u] = true;
-    } else if constexpr (SMODE == 1) {
+    } else if constexpr (BLK) {
       // Only the tile's BN/128 column blocks are read; the other lanes repeat
       // the last one (one cache line per step instead of 64).
       const int nb = min(n0 / 128 + min(lane, (BN + 127) / 128 - 1), (N + 127) / 128 - 1);
@@ -288,7 +313,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
   // one wave per SIMD nothing else hides that latency).  Same products and
   // association, so the same results.  pd/sd: the deferred partials and
   // scales (zero before the first step: acc + 0*0 = acc).
-  constexpr bool DEFER = SMODE >= 1 && FM * FN * MM::NACC <= 32;
+  constexpr bool DEFER = (SMODE == 1 || SMODE == 2) && FM * FN * MM::NACC <= 32;
   // Block mode with deferred folds forms the row-scale products once per
   // wave in LDS (the wave's TM products, one per lane) rather than once per
   // accumulator row in every lane.
@@ -343,7 +368,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
     const uint8_t* st = smem + soff;
     const uint8_t* sA = st;
     const uint8_t* sB = st + A_BYTES;
-    if constexpr (SMODE == 0) {
+    if constexpr (SMODE == 0 || SMODE == 3) {
+      // Power-of-two block scales: this lane's A row exponent per M tile and
+      // the wave's column block exponent (one 128 block per wave).
+      int ea[FM], ebv = 127;
+      if constexpr (SMODE == 3) {
+        const float* sS = (const float*)(st + A_BYTES + B_BYTES);
+        ebv = e8m0_of(sS[NI_SA * 64 + (wn * TN) / 128]);
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) ea[fm] = e8m0_of(sS[wm * TM + fm * MF + lane % MF]);
+      }
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int c0 = MM::chunk(ks, lane);
@@ -365,9 +399,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-          for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = MM::mma(af[fm], bf[fn], acc[fm][fn]);
+          for (int fn = 0; fn < FN; ++fn) {
+            if constexpr (SMODE == 3) acc[fm][fn] = MM::mma_s(af[fm], bf[fn], acc[fm][fn], ea[fm], ebv);
+            else acc[fm][fn] = MM::mma(af[fm], bf[fn], acc[fm][fn]);
+          }
       }
-    } else if constexpr (SMODE == 2) {
+    } else if constexpr (F4) {
       const float* sS = (const float*)(st + A_BYTES + B_BYTES);
       const uint32_t* sE = (const uint32_t*)(st + A_BYTES + B_BYTES + SA_ROWS);
       // B fragments (16 bytes = 32 e2m1 values per lane) and their e8m0 block
@@ -395,6 +432,15 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
           const i32x4 lo = *(const i32x4*)(sA + swz<BK>(r, c0));
           const i32x4 hi = *(const i32x4*)(sA + swz<BK>(r, c0 + MM::CHUNK_A4_HI));
           af[ks] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+        if constexpr (PW2) {
+          // power-of-two activation scales: the MFMA applies both exponents
+          const int ea = e8m0_of(sS[wm * TM + fm * MF + lane % MF]);
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) acc[fm][fn] = MM::mma4_s(af[ks], bf[ks][fn], acc[fm][fn], ea, eb[ks][fn]);
+          continue;
         }
         float srow[MM::NACC];
 #pragma unroll
@@ -638,8 +684,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 template <int BM, int BN, int BK, int WGN, int R, int SMODE>
 constexpr int cfg_lds() {
   const int sa = SMODE >= 1 ? ((BM * 4 + 255) / 256) * 256 : 0;
-  const int sb = SMODE == 1 ? 256 : (SMODE == 2 ? ((BN * 4 + 255) / 256) * 256 : 0);
-  return R * (BM * BK + BN * (SMODE == 2 ? BK / 2 : BK) + sa + sb) + (SMODE == 1 ? WGN * BM * 4 : 0);
+  constexpr bool f4 = SMODE == 2 || SMODE == 4;
+  const int sb = (SMODE == 1 || SMODE == 3) ? 256 : (f4 ? ((BN * 4 + 255) / 256) * 256 : 0);
+  return R * (BM * BK + BN * (f4 ? BK / 2 : BK) + sa + sb) + (SMODE == 1 ? WGN * BM * 4 : 0);
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, int MF, int R, int SMODE, int ODT>
@@ -665,7 +712,7 @@ void launch_grouped_cfg(const GemmArgs& x, int max_mtiles, hipStream_t stream) {
 
 template <int SMODE, int ODT>
 void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
-  if constexpr (SMODE == 2) {
+  if constexpr (SMODE == 2 || SMODE == 4) {
     // MXFP4 B: the 128-wide K step kinds (the e2m1 slab is half as large, so
     // 256x256 takes three stages).
     switch (p.kind) {
@@ -702,7 +749,7 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
       case 16: launch_cfg<256, 256, 128, 2, 4, 16, 2, SMODE, ODT>(p, x, stream); break;
       case 17: launch_cfg<128, 256, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
       case 14:
-        if constexpr (SMODE == 0) launch_cfg<256, 256, 128, 4, 4, 32, 2, SMODE, ODT>(p, x, stream);
+        if constexpr (SMODE == 0 || SMODE == 3) launch_cfg<256, 256, 128, 4, 4, 32, 2, SMODE, ODT>(p, x, stream);
         break;
       default: launch_cfg<256, 128, 128, 4, 2, 32, 3, SMODE, ODT>(p, x, stream); break;
     }
@@ -722,6 +769,11 @@ int env_int(const char* name, int dflt) {
 GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   GemmPlan p;
   const int KT = K / 128;
+  // Power-of-two block FP8 runs the per-token loop (the MFMA applies the
+  // scales; no fold), so it takes the per-token plan; power-of-two MXFP4 the
+  // MXFP4 plan.
+  if (smode == 3) smode = 0;
+  if (smode == 4) smode = 2;
   // Measured on MI355X at the Llama-3-70B / DeepSeek-V3 shapes (BASELINE
   // configs 2 and 3): skinny M streams B with 16- to 64-row tiles, split over
   // K when too few column tiles cover the 256 CUs; larger M takes the largest
@@ -824,6 +876,8 @@ void launch_grouped_smode(int kind, const GemmArgs& x, int max_mtiles, hipStream
 
 void launch_gemm_grouped(int kind, int smode, const GemmArgs& x, int max_mtiles, hipStream_t stream) {
   if (smode == 2) launch_grouped_smode<2>(kind, x, max_mtiles, stream);
+  else if (smode == 3) launch_grouped_smode<3>(kind, x, max_mtiles, stream);
+  else if (smode == 4) launch_grouped_smode<4>(kind, x, max_mtiles, stream);
   else launch_grouped_smode<1>(kind, x, max_mtiles, stream);
 }
 
@@ -852,6 +906,12 @@ void launch_gemm(const GemmPlan& p, int smode, int odt, const GemmArgs& x, hipSt
   } else if (smode == 2) {
     if (odt == TI_DTYPE_F16) launch_kind<2, TI_DTYPE_F16>(p, x, stream);
     else launch_kind<2, TI_DTYPE_BF16>(p, x, stream);
+  } else if (smode == 3) {
+    if (odt == TI_DTYPE_F16) launch_kind<3, TI_DTYPE_F16>(p, x, stream);
+    else launch_kind<3, TI_DTYPE_BF16>(p, x, stream);
+  } else if (smode == 4) {
+    if (odt == TI_DTYPE_F16) launch_kind<4, TI_DTYPE_F16>(p, x, stream);
+    else launch_kind<4, TI_DTYPE_BF16>(p, x, stream);
   } else {
     if (odt == TI_DTYPE_F16) launch_kind<1, TI_DTYPE_F16>(p, x, stream);
     else launch_kind<1, TI_DTYPE_BF16>(p, x, stream);
@@ -884,7 +944,7 @@ static int gemm_common(const char* name, int smode, const uint8_t* a, const floa
   GemmArgs x{};
   x.a = a; x.b = b; x.sa = a_scale; x.sb = b_scale;
   x.sa_stride = a_scale_stride; x.sb_stride = b_scale_stride;
-  x.sb_layout = smode == 2 ? b_scale_stride : 0;
+  x.sb_layout = (smode == 2 || smode == 4) ? b_scale_stride : 0;
   x.b_tiled = b_tiled;
   x.sa_layout = smode >= 1 ? a_scale_layout : 0;
   x.out = (uint16_t*)out;
@@ -979,6 +1039,24 @@ extern "C" int ti_fp8_gemm_block(const uint8_t* a, const float* a_scale, int a_s
   TI_CHECK_ARG(a_scale_layout == 0 || a_scale_layout == 1, "ti_fp8_gemm_block: a_scale_layout must be 0 or 1");
   return gemm_common("ti_fp8_gemm_block", 1, a, a_scale, 0, b, b_scale, 0, out, out_dtype, M, N, K, workspace,
                      workspace_bytes, stream, a_scale_layout);
+}
+
+extern "C" int ti_fp8_gemm_block_pow2(const uint8_t* a, const float* a_scale, int a_scale_layout,
+                                      const uint8_t* b, const float* b_scale, void* out, int out_dtype, int M,
+                                      int N, int K, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  TI_CHECK_ARG(a_scale_layout == 0 || a_scale_layout == 1,
+               "ti_fp8_gemm_block_pow2: a_scale_layout must be 0 or 1");
+  return gemm_common("ti_fp8_gemm_block_pow2", 3, a, a_scale, 0, b, b_scale, 0, out, out_dtype, M, N, K,
+                     workspace, workspace_bytes, stream, a_scale_layout);
+}
+
+extern "C" int ti_fp4_gemm_pow2(const uint8_t* a, const float* a_scale, int a_scale_layout, const uint8_t* b,
+                                const uint8_t* b_scale, int b_scale_layout, void* out, int out_dtype, int M, int N,
+                                int K, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  TI_CHECK_ARG(a_scale_layout == 0 || a_scale_layout == 1, "ti_fp4_gemm_pow2: a_scale_layout must be 0 or 1");
+  TI_CHECK_ARG(b_scale_layout == 0 || b_scale_layout == 1, "ti_fp4_gemm_pow2: b_scale_layout must be 0 or 1");
+  return gemm_common("ti_fp4_gemm_pow2", 4, a, a_scale, 0, b, (const float*)b_scale, b_scale_layout, out,
+                     out_dtype, M, N, K, workspace, workspace_bytes, stream, a_scale_layout);
 }
 
 extern "C" int ti_fp4_gemm(const uint8_t* a, const float* a_scale, int a_scale_layout, const uint8_t* b,

@@ -473,7 +473,9 @@ extern "C" size_t ti_fp8_moe_workspace_bytes(int T, int k, int E, int H, int I) 
 
 // Routed experts, shared by the block-FP8 (smode 1: e4m3 weights, 128x128
 // fp32 scales) and MXFP4 (smode 2: e2m1 weights two per byte, e8m0 scale per
-// 32 K) weight formats; activations are 1x128 block FP8 in both.
+// 32 K) weight formats; activations are 1x128 block FP8 in both.  With
+// round_scale 2 every scale is a power of two and the grouped GEMMs apply
+// them inside the MFMA (smode 3 / 4).
 static int moe_run(const char* name, int smode, int sb_layout, const void* hidden, const float* topk_weights,
                    const int32_t* topk_ids, int T, int k, const uint8_t* w13, const void* s13, const uint8_t* w2,
                    const void* s2, int E, int H, int I, float clamp_limit, int round_scale, void* out,
@@ -485,7 +487,9 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
   TI_CHECK_ARG(((uintptr_t)hidden & 15) == 0 && ((uintptr_t)w13 & 15) == 0 && ((uintptr_t)w2 & 15) == 0 &&
                    ((uintptr_t)out & 3) == 0 && ((uintptr_t)s13 & 3) == 0 && ((uintptr_t)s2 & 3) == 0,
                "%s: hidden, w13, w2 must be 16-byte and out, scales 4-byte aligned", name);
+  TI_CHECK_ARG(round_scale >= 0 && round_scale <= 2, "%s: round_scale must be 0, 1 or 2", name);
   if (T == 0) return TI_OK;
+  if (round_scale == 2) smode += 2;
   Plan p = make_plan(T, k, E, smode);
   Ws w = carve(nullptr, T, k, E, H, I, p);
   if (!workspace || workspace_bytes < w.bytes) {
@@ -495,7 +499,7 @@ static int moe_run(const char* name, int smode, int sb_layout, const void* hidde
   TI_CHECK_ARG(((uintptr_t)workspace & 255) == 0, "%s: workspace must be 256-byte aligned", name);
   w = carve((uint8_t*)workspace, T, k, E, H, I, p);
   const long R = (long)T * k;
-  const bool f4 = smode == 2;
+  const bool f4 = smode == 2 || smode == 4;
 
   // 1. hidden -> e4m3 1x128
   int st = ti_fp8_quant_block(hidden, TI_DTYPE_BF16, T, H, 128, round_scale ? 1 : 0, w.xq, w.xs, 0, stream);

@@ -12,17 +12,29 @@ libti_quant.so's gfx950 kernels.  Block scales may be stored as fp32 or, as the
 reference's ``scale_dtype=float8_e8m0fnu`` (tensor_parallel.py:1211-1212), as
 E8M0 bytes: those are powers of two, widened to fp32 exactly before the GEMM;
 E8M0 activation scales are produced only with a ``scale_fmt`` (power-of-two
-scales), the only combination the reference model configures.
+scales), the only combination the reference model configures.  When every scale
+of a GEMM is a power of two -- ``scale_dtype=float8_e8m0fnu``, or ``linear`` with a
+``scale_fmt`` and E8M0 weight scales (MXFP4 weights always have them) -- the GEMM
+applies the scales as MFMA exponents (``ti_fp8_gemm_block_pow2`` /
+``ti_fp4_gemm_pow2``) instead of folding each 128-K partial sum in fp32.
 """
 from __future__ import annotations
 
 import torch
 from torch import Tensor
 
+import os
+
 from .. import _lib
 from .fp8 import FP8_E4M3, _ws_args
 
 BLOCK = 128
+
+
+def _pow2_enabled() -> bool:
+    """Power-of-two (E8M0) scales go to the GEMMs that apply them inside the MFMA
+    unless ``TI_ROCM_POW2_MFMA=0`` (then the fp32-scale GEMMs run them)."""
+    return os.environ.get("TI_ROCM_POW2_MFMA", "1") != "0"
 
 
 E8M0 = torch.float8_e8m0fnu
@@ -105,6 +117,7 @@ def fp8_gemm(
         raise ValueError("FP8 GEMM operands must be float8_e4m3fn")
     if a_s.dtype != scale_dtype or b_s.dtype != scale_dtype:
         raise ValueError("FP8 GEMM scales must have the given scale_dtype")
+    pow2 = scale_dtype == E8M0
     a_s, b_s = _f32_scales(a_s), _f32_scales(b_s)
     _lib.require_device(a, a_s, b, b_s)
     k = a.size(-1)
@@ -114,19 +127,23 @@ def fp8_gemm(
         raise ValueError("FP8 GEMM weight must be [N, K] with the activation's K")
     if a_s.numel() != m * (k // BLOCK) or tuple(b_s.shape) != (-(-n // BLOCK), -(-k // BLOCK)):
         raise ValueError("FP8 GEMM block scales must be a_s [M, K/128] and b_s [ceil(N/128), K/128]")
-    return _fp8_gemm_raw(a, a_s, 0, b, b_s)
+    return _fp8_gemm_raw(a, a_s, 0, b, b_s, pow2)
 
 
-def _fp8_gemm_raw(a: Tensor, a_s: Tensor, a_layout: int, b: Tensor, b_s: Tensor) -> Tensor:
+def _fp8_gemm_raw(a: Tensor, a_s: Tensor, a_layout: int, b: Tensor, b_s: Tensor, pow2: bool = False) -> Tensor:
+    """Block GEMM; ``pow2``: every scale is a power of two (E8M0 values), which
+    ``ti_fp8_gemm_block_pow2`` applies inside the MFMA."""
     k = a.size(-1)
     m = a.numel() // k
     n = b.size(0)
     out = torch.empty((*a.shape[:-1], n), dtype=torch.bfloat16, device=a.device)
     if m == 0:
         return out
-    ws, ws_bytes = _ws_args(a.device, m, n, k, 1)
-    _lib.call("ti_fp8_gemm_block", a.data_ptr(), a_s.data_ptr(), a_layout, b.data_ptr(), b_s.data_ptr(),
-              out.data_ptr(), _lib.TI_DTYPE_BF16, m, n, k, ws, ws_bytes, _lib.stream_of(a))
+    pow2 = pow2 and _pow2_enabled()
+    ws, ws_bytes = _ws_args(a.device, m, n, k, 3 if pow2 else 1)
+    _lib.call("ti_fp8_gemm_block_pow2" if pow2 else "ti_fp8_gemm_block", a.data_ptr(), a_s.data_ptr(), a_layout,
+              b.data_ptr(), b_s.data_ptr(), out.data_ptr(), _lib.TI_DTYPE_BF16, m, n, k, ws, ws_bytes,
+              _lib.stream_of(a))
     return out
 
 
@@ -183,16 +200,19 @@ def fp4_scale_stepmajor(scale_bytes: Tensor) -> Tensor:
     return dst.view(*lead, kb // 4, n, 4)
 
 
-def _fp4_gemm_raw(a: Tensor, a_s: Tensor, a_layout: int, b: Tensor, eb: Tensor, layout: int, n: int) -> Tensor:
+def _fp4_gemm_raw(a: Tensor, a_s: Tensor, a_layout: int, b: Tensor, eb: Tensor, layout: int, n: int,
+                  pow2: bool = False) -> Tensor:
+    """MXFP4 GEMM; ``pow2``: the activation scales are powers of two, which
+    ``ti_fp4_gemm_pow2`` applies inside the MFMA with the weight's."""
     k = a.size(-1)
     m = a.numel() // k
     out = torch.empty((*a.shape[:-1], n), dtype=torch.bfloat16, device=a.device)
     if m == 0:
         return out
-    ws, ws_bytes = _ws_args(a.device, m, n, k, 2)
-    _lib.call("ti_fp4_gemm", a.data_ptr(), a_s.data_ptr(), a_layout, b.data_ptr(), eb.data_ptr(), layout,
-              out.data_ptr(),
-              _lib.TI_DTYPE_BF16, m, n, k, ws, ws_bytes, _lib.stream_of(a))
+    pow2 = pow2 and _pow2_enabled()
+    ws, ws_bytes = _ws_args(a.device, m, n, k, 4 if pow2 else 2)
+    _lib.call("ti_fp4_gemm_pow2" if pow2 else "ti_fp4_gemm", a.data_ptr(), a_s.data_ptr(), a_layout, b.data_ptr(),
+              eb.data_ptr(), layout, out.data_ptr(), _lib.TI_DTYPE_BF16, m, n, k, ws, ws_bytes, _lib.stream_of(a))
     return out
 
 
@@ -213,6 +233,7 @@ def fp4_gemm(
         raise ValueError("FP4 GEMM operands must be float8_e4m3fn activations and float4_e2m1fn_x2 weights")
     if a_s.dtype != scale_dtype:
         raise ValueError("FP4 GEMM activation scales must have the given scale_dtype")
+    pow2 = scale_dtype == E8M0
     a_s = _f32_scales(a_s)
     _lib.require_device(a, a_s, b, b_s)
     k = a.size(-1)
@@ -225,7 +246,7 @@ def fp4_gemm(
     eb = e8m0_bytes(b_s)
     if a_s.numel() != m * (k // BLOCK) or tuple(eb.shape) != (n, k // 32):
         raise ValueError("FP4 GEMM scales must be a_s [M, K/128] and b_s [N, K/32]")
-    return _fp4_gemm_raw(a, a_s, 0, b, eb, 0, n)
+    return _fp4_gemm_raw(a, a_s, 0, b, eb, 0, n, pow2)
 
 
 def linear(x: Tensor, weight: Tensor, weight_scale: Tensor, scale_fmt: str | None = None,
@@ -254,7 +275,7 @@ def linear(x: Tensor, weight: Tensor, weight_scale: Tensor, scale_fmt: str | Non
         if x.size(-1) != weight.size(1) * 2:
             raise ValueError("MXFP4 weight K does not match the activation")
         xq, xs = _act_quant_stepmajor(x, round_scale)
-        return _fp4_gemm_raw(xq, xs, 1, weight, cached[1], 1, weight.size(0))
+        return _fp4_gemm_raw(xq, xs, 1, weight, cached[1], 1, weight.size(0), round_scale)
     if weight.dtype != FP8_E4M3 or weight_scale.dtype not in (torch.float32, E8M0):
         raise ValueError("block-FP8 linear needs a float8_e4m3fn weight with fp32 or E8M0 block scales")
     k = x.size(-1)
@@ -266,4 +287,5 @@ def linear(x: Tensor, weight: Tensor, weight_scale: Tensor, scale_fmt: str | Non
     _lib.require_device(weight, weight_scale)
     sb = _weight_scales_f32(weight, weight_scale)
     xq, xs = _act_quant_stepmajor(x, round_scale)
-    return _fp8_gemm_raw(xq, xs, 1, weight.contiguous(), sb.contiguous())
+    # ue8m0 activations with E8M0 weight scales: all scales are powers of two
+    return _fp8_gemm_raw(xq, xs, 1, weight.contiguous(), sb.contiguous(), round_scale and weight_scale.dtype == E8M0)

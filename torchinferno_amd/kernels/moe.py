@@ -25,7 +25,7 @@ import torch
 from torch import Tensor
 
 from .. import _lib
-from .block_fp8 import FP4, e8m0_bytes, fp4_scale_stepmajor
+from .block_fp8 import E8M0, FP4, _pow2_enabled, e8m0_bytes, fp4_scale_stepmajor
 from .fp8 import FP8_E4M3
 
 _ws_lock = threading.Lock()
@@ -44,6 +44,20 @@ class PreparedFp8Experts:
     global_num_experts: int
     hidden_size: int
     intermediate_size: int
+    scales_pow2: bool = False  # every block scale a power of two (E8M0 values)
+
+
+def _all_pow2(*scales: Tensor) -> bool:
+    """True when every scale is a power of two in the E8M0 range (2^-127..2^127):
+    E8M0 storage always, fp32 when each value is (one pass at weight preparation)."""
+    for s in scales:
+        if s.dtype == E8M0:
+            continue
+        f = s.float()
+        m, e = torch.frexp(f)
+        if not bool(((m == 0.5) & (f >= 2.0 ** -127)).all()):
+            return False
+    return True
 
 
 def prepare_fp8_experts(w1: Tensor, w3: Tensor, w2: Tensor, w1_scale: Tensor, w3_scale: Tensor,
@@ -51,7 +65,8 @@ def prepare_fp8_experts(w1: Tensor, w3: Tensor, w2: Tensor, w1_scale: Tensor, w3
                         global_num_experts: int | None = None) -> PreparedFp8Experts:
     """Stack one GPU's block-FP8 experts (the analogue of prepare_mxfp4_experts,
     deepseek_v4_marlin.py:194-264).  ``w1``/``w3`` e4m3 ``[E, I, H]``, ``w2`` ``[E, H, I]``,
-    scales fp32 per 128x128 block.  Weight preparation: run once, before capture."""
+    scales per 128x128 block, fp32 or ``float8_e8m0fnu``.  Weight preparation: run
+    once, before capture."""
     if w1.ndim != 3 or w3.ndim != 3 or w2.ndim != 3:
         raise ValueError("expert weights must be stacked [experts, output, K]")
     if tuple(w1.shape) != tuple(w3.shape):
@@ -68,13 +83,14 @@ def prepare_fp8_experts(w1: Tensor, w3: Tensor, w2: Tensor, w1_scale: Tensor, w3
     expert_map[expert_start:expert_start + e] = torch.arange(e, dtype=torch.int32, device=w1.device)
     return PreparedFp8Experts(
         w13=torch.cat((w1, w3), dim=1).contiguous(),
-        w13_scale=torch.cat((w1_scale, w3_scale), dim=1).float().contiguous(),
+        w13_scale=torch.cat((w1_scale.float(), w3_scale.float()), dim=1).contiguous(),
         w2=w2.contiguous(),
         w2_scale=w2_scale.float().contiguous(),
         expert_map=expert_map,
         global_num_experts=global_num_experts,
         hidden_size=hidden,
         intermediate_size=inter,
+        scales_pow2=_all_pow2(w1_scale, w3_scale, w2_scale),
     )
 
 
@@ -157,10 +173,14 @@ def _workspace(device: torch.device, nbytes: int) -> Tensor:
         return ws
 
 
-def _round_scale(scale_fmt: str | None) -> int:
+def _round_scale(scale_fmt: str | None, weight_scales_pow2: bool) -> int:
     """act_quant's ``scale_fmt`` (deepseek_v4_tilelang_definitions.py:255-331): any
-    format rounds the 1x128 activation scales up to powers of two."""
-    return int(scale_fmt is not None)
+    format rounds the 1x128 activation scales up to powers of two (1); with
+    power-of-two weight scales too, the kernels apply all of them inside the
+    MFMA (2)."""
+    if scale_fmt is None:
+        return 0
+    return 2 if weight_scales_pow2 and _pow2_enabled() else 1
 
 
 def _routed(entry: str, hidden_states: Tensor, topk_weights: Tensor, topk_ids: Tensor, experts,
@@ -191,7 +211,7 @@ def _routed(entry: str, hidden_states: Tensor, topk_weights: Tensor, topk_ids: T
     _lib.call(entry, hidden_states.data_ptr(), weights.data_ptr(), local_ids.data_ptr(), tokens, k,
               experts.w13.data_ptr(), experts.w13_scale.data_ptr(), experts.w2.data_ptr(),
               experts.w2_scale.data_ptr(), *layout, e_local, hidden, inter, float(clamp_limit),
-              _round_scale(scale_fmt), out.data_ptr(),
+              _round_scale(scale_fmt, entry == "ti_fp4_moe" or experts.scales_pow2), out.data_ptr(),
               aligned, ws.numel() - (aligned - base), _lib.stream_of(hidden_states))
     return out
 
