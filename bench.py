@@ -455,9 +455,10 @@ def fp8_single_point(spec, launches, dev, stream):
     print(json.dumps({"point": spec, "launches": launches}), flush=True)
 
 
-def moe_single_point(t, launches, dev, stream):
+def moe_single_point(t, launches, dev, stream, ue8m0=False):
     """Launch the config-4 routed FP8 MoE (router included) at T tokens `launches`
-    times: the program a kernel-trace run profiles."""
+    times: the program a kernel-trace run profiles.  ``ue8m0``: DeepSeek-V4's scale
+    format (power-of-two activation and E8M0 weight scales, applied by the MFMA)."""
     import torch
     from torchinferno_amd import _lib
     L = _lib.lib()
@@ -466,6 +467,8 @@ def moe_single_point(t, launches, dev, stream):
     w2 = torch.randint(-120, 120, (e, h, inter), device=dev, dtype=torch.int8)
     s13 = torch.rand((e, 2 * inter // 128, h // 128), device=dev) * 1e-3 + 1e-4
     s2 = torch.rand((e, h // 128, inter // 128), device=dev) * 1e-3 + 1e-4
+    if ue8m0:
+        s13, s2 = (torch.exp2(torch.randint(-13, -9, s.shape, device=dev).float()) for s in (s13, s2))
     x = torch.randn((t, h), device=dev).to(torch.bfloat16)
     logits = torch.randn((t, e), device=dev)
     wts = torch.empty((t, k), dtype=torch.float32, device=dev)
@@ -478,10 +481,10 @@ def moe_single_point(t, launches, dev, stream):
         _check("route", L.ti_moe_route_topk(logits.data_ptr(), t, e, k, 1, 1.0, wts.data_ptr(), ids.data_ptr(),
                                             stream))
         _check("moe", L.ti_fp8_moe(x.data_ptr(), wts.data_ptr(), ids.data_ptr(), t, k, w13.data_ptr(),
-                                   s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), e, h, inter, 0.0, 0,
-                                   out.data_ptr(), wsp, need, stream))
+                                   s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), e, h, inter, 0.0,
+                                   2 if ue8m0 else 0, out.data_ptr(), wsp, need, stream))
     torch.cuda.synchronize()
-    print(json.dumps({"point": f"moe:{t}", "launches": launches}), flush=True)
+    print(json.dumps({"point": f"moe:{t}" + (":ue8m0" if ue8m0 else ""), "launches": launches}), flush=True)
 
 
 # --------------------------------------------------------------------------- fused producers
@@ -618,6 +621,7 @@ def main():
     ap.add_argument("--point", default=None,
                     help="NAME:M -- launch only that config-1 int4 point, --steps times (counter runs); "
                          "rowcol:SHAPE:M / block:SHAPE:M for a config-2 / config-3 FP8 GEMM; "
+                         "moe:T[:ue8m0] for the config-4 MoE; "
                          "'copy' for a 256 MiB copy (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -647,7 +651,8 @@ def main():
         print(json.dumps({"point": "copy", "bytes_read": src.numel() * 4, "launches": args.steps}), flush=True)
         return
     if args.point and args.point.startswith("moe:"):
-        moe_single_point(int(args.point.split(":")[1]), args.steps, dev, stream)
+        f = args.point.split(":")
+        moe_single_point(int(f[1]), args.steps, dev, stream, ue8m0=f[2:] == ["ue8m0"])
         return
     if args.point and args.point.count(":") == 2:
         fp8_single_point(args.point, args.steps, dev, stream)

@@ -46,7 +46,8 @@ def test_fp4_gemm_matches_oracle(dev, m, n, k):
     assert _rel_err(y.float().cpu().numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("kind", ["1", "2", "3", "5", "6", "9", "10", "11", "12", "13", "15", "16", "17"])
+@pytest.mark.parametrize("kind", ["1", "2", "3", "5", "6", "9", "10", "11", "12", "13", "15", "16", "17", "18",
+                                  "19", "20"])
 @pytest.mark.parametrize("splits", ["1", "3"])
 def test_fp4_gemm_every_kind(dev, monkeypatch, kind, splits):
     """Both scale layouts: the checkpoint's [N, K/32] and the step-major copy."""
@@ -140,7 +141,7 @@ def _mxfp4_experts(e, h, inter, seed, dev):
 
 
 @pytest.mark.parametrize("t,k", [(1, 1), (9, 2), (64, 4), (300, 8)])
-@pytest.mark.parametrize("kind", ["auto", "2", "5", "6", "9", "11", "12", "13", "15", "17"])
+@pytest.mark.parametrize("kind", ["auto", "2", "5", "6", "9", "11", "12", "13", "15", "17", "20"])
 def test_mxfp4_moe_matches_oracle(dev, monkeypatch, t, k, kind):
     from torchinferno_amd.kernels import moe as tmoe
     print(f"[fp4] moe T={t} k={k} kind={kind}", flush=True)
@@ -162,11 +163,11 @@ def test_mxfp4_moe_matches_oracle(dev, monkeypatch, t, k, kind):
 
 
 def test_mxfp4_moe_tile_boundaries(dev, monkeypatch):
-    """MXFP4 experts whose row counts sit on the m-tile boundaries: the two-tier
-    128-row tile (kind 17) against the single-tier 128x128 tile (kind 15, to a
-    bf16-rounding bound) and the oracle."""
+    """MXFP4 experts whose row counts sit on the m-tile boundaries of the two-tier
+    plans (128-row first tier, 192- or 256-row second tier) against the single-tier
+    128x128 tile (kind 15, to a bf16-rounding bound) and the oracle."""
     from torchinferno_amd.kernels import moe as tmoe
-    counts = [0, 1, 128, 129, 255, 256, 257, 385]
+    counts = [0, 1, 128, 129, 192, 193, 255, 256, 257, 321, 385]
     e, h, inter = len(counts), 512, 256
     ex = _mxfp4_experts(e, h, inter, 21, dev)
     ids_np = np.concatenate([np.full(c, i, dtype=np.int32) for i, c in enumerate(counts)])
@@ -177,10 +178,12 @@ def test_mxfp4_moe_tile_boundaries(dev, monkeypatch):
     ids = torch.from_numpy(ids_np).to(dev).view(t, 1)
     w = (torch.rand((t, 1), generator=g, device=dev) + 0.5).float()
     ys = {}
-    for kind in ("17", "15"):
-        print(f"[fp4] moe tile boundaries kind={kind}", flush=True)
+    for plan in ("15", "20/19", "17/18", "17/16"):
+        print(f"[fp4] moe tile boundaries plan={plan}", flush=True)
+        kind, _, kind2 = plan.partition("/")
         monkeypatch.setenv("TI_ROCM_MOE_KIND", kind)
-        ys[kind] = tmoe.fused_mxfp4_moe(x, w, ids, ex).float().cpu().numpy()
+        monkeypatch.setenv("TI_ROCM_MOE_KIND2", kind2)
+        ys[plan] = tmoe.fused_mxfp4_moe(x, w, ids, ex).float().cpu().numpy()
 
     def rows(st):  # step-major [K/128, N, 4] -> checkpoint [N, K/32]
         return st.permute(1, 0, 2).reshape(st.size(1), -1).cpu().numpy()
@@ -188,8 +191,9 @@ def test_mxfp4_moe_tile_boundaries(dev, monkeypatch):
                for i in range(e)]
     ref = omoe.moe_reference(x.float().cpu().numpy(), w.cpu().numpy(), ids_np.reshape(t, 1), experts,
                              linear=omoe.mxfp4_linear)
-    assert _rel_err(ys["17"], ref) <= TOL
-    for i, c in enumerate(counts):
-        r = ids_np == i
-        if r.any():
-            assert np.abs(ys["17"][r] - ys["15"][r]).max() <= 2 ** -7 * np.abs(ys["15"][r]).max(), c
+    for plan, y in ys.items():
+        assert _rel_err(y, ref) <= TOL, plan
+        for i, c in enumerate(counts):
+            r = ids_np == i
+            if r.any():
+                assert np.abs(y[r] - ys["15"][r]).max() <= 2 ** -7 * np.abs(ys["15"][r]).max(), (plan, c)

@@ -101,7 +101,7 @@ def test_router_options(dev):
 
 
 @pytest.mark.parametrize("t,k", [(1, 1), (7, 2), (64, 4), (300, 8)])
-@pytest.mark.parametrize("kind", ["auto", "2", "5", "6", "9", "11", "12", "13", "15", "17"])
+@pytest.mark.parametrize("kind", ["auto", "2", "5", "6", "9", "11", "12", "13", "15", "17", "20"])
 def test_moe_small_matches_oracle(dev, monkeypatch, t, k, kind):
     from torchinferno_amd.kernels import moe as tmoe
     print(f"[moe] small T={t} k={k} kind={kind}", flush=True)
@@ -121,15 +121,17 @@ def test_moe_small_matches_oracle(dev, monkeypatch, t, k, kind):
 
 
 def test_moe_tile_boundaries(dev, monkeypatch):
-    """Experts whose row counts sit on the m-tile boundaries (0, 1, 128, 129, 255,
-    256, 257, 385 and 512 rows).  With the 128-row tile (kind 17) an expert's rows
-    split into 256-row tiles plus at most one 128-row tile; that result must agree
-    with the single-tier 128x128 tile (kind 15) to a bf16-rounding bound, and both
-    with the oracle.  (Against the oracle, a few hidden-row e4m3 codes flip between
-    the two sides' fp32 rounding orders; at K = 1024 that moves an output by up to
-    about 1.2% of the output scale, hence MOE_TOL there.)"""
+    """Experts whose row counts sit on the m-tile boundaries of every two-tier plan
+    (0, 1, 128, 129, 192, 193, 255, 256, 257, 320, 321, 385 and 512 rows).  With a
+    128-row first tier (kinds 17, 20) an expert's rows split into second-tier tiles
+    (192 rows: kinds 18, 19; 256: kind 16) plus at most one 128-row tile; each plan
+    must agree with the single-tier 128x128 tile (kind 15) to a bf16-rounding bound,
+    and with the oracle.  (Against the oracle, a few hidden-row e4m3 codes flip
+    between the two sides' fp32 rounding orders; at K = 1024 a flip moves an output
+    by up to about 2% of the expert's output scale, so there the bar is: every
+    element within 2 * MOE_TOL, 99% of them within MOE_TOL / 4.)"""
     from torchinferno_amd.kernels import moe as tmoe
-    counts = [0, 1, 128, 129, 255, 256, 257, 385, 512]
+    counts = [0, 1, 128, 129, 192, 193, 255, 256, 257, 320, 321, 385, 512]
     e, h, inter = len(counts), 1024, 512
     experts = _make_experts(e, h, inter, 17, dev)
     ids_np = np.concatenate([np.full(c, i, dtype=np.int32) for i, c in enumerate(counts)])
@@ -140,19 +142,23 @@ def test_moe_tile_boundaries(dev, monkeypatch):
     ids = torch.from_numpy(ids_np).to(dev).view(t, 1)
     w = (torch.rand((t, 1), generator=g, device=dev) + 0.5).float()
     ys = {}
-    for kind in ("17", "15"):
-        print(f"[moe] tile boundaries kind={kind}", flush=True)
+    for plan in ("15", "20/19", "17/16", "17/18", "20/16"):
+        print(f"[moe] tile boundaries plan={plan}", flush=True)
+        kind, _, kind2 = plan.partition("/")
         monkeypatch.setenv("TI_ROCM_MOE_KIND", kind)
-        ys[kind] = tmoe.fused_fp8_moe(x, w, ids, experts).float().cpu().numpy()
+        monkeypatch.setenv("TI_ROCM_MOE_KIND2", kind2)
+        ys[plan] = tmoe.fused_fp8_moe(x, w, ids, experts).float().cpu().numpy()
     ref = _oracle_tokens(x, w, ids, experts, np.arange(t))
     for i, c in enumerate(counts):
         rows = ids_np == i
         if not rows.any():
             continue
-        y17, y15 = ys["17"][rows], ys["15"][rows]
-        # same rows, other tiling: at most bf16 rounding apart
-        assert np.abs(y17 - y15).max() <= 2 ** -7 * np.abs(y15).max(), c
-        assert _rel_err(y17, ref[rows]) <= MOE_TOL, c
+        y15 = ys["15"][rows]
+        for plan, y in ys.items():
+            # same rows, other tiling: at most bf16 rounding apart
+            assert np.abs(y[rows] - y15).max() <= 2 ** -7 * np.abs(y15).max(), (plan, c)
+            d = np.abs(y[rows] - ref[rows]) / np.abs(ref[rows]).max()
+            assert d.max() <= 2 * MOE_TOL and np.percentile(d, 99) <= MOE_TOL / 4, (plan, c, d.max())
 
 
 def test_moe_one_expert_is_dense_ffn(dev):

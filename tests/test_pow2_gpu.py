@@ -64,7 +64,7 @@ def _check_block(y, a, a_s, codes, s):
     return elementwise_ratio(y.float().cpu().numpy(), ref, ref_abs)
 
 
-@pytest.mark.parametrize("kind", range(18))
+@pytest.mark.parametrize("kind", range(21))
 def test_block_pow2_every_kind(dev, monkeypatch, kind):
     from torchinferno_amd.kernels import block_fp8 as tb
     a, a_s, b, b_s, codes, s = _block_problem(200, 1280, 400, 50 + kind, dev)
@@ -123,7 +123,8 @@ def _fp4_inputs(m, n, k, seed, dev):
     return (a, a_s, b, b_s), t
 
 
-@pytest.mark.parametrize("kind", ["1", "2", "3", "5", "6", "9", "10", "11", "12", "13", "15", "16", "17"])
+@pytest.mark.parametrize("kind", ["1", "2", "3", "5", "6", "9", "10", "11", "12", "13", "15", "16", "17", "18",
+                                  "19", "20"])
 def test_fp4_pow2_every_kind(dev, monkeypatch, kind):
     from torchinferno_amd.kernels import block_fp8 as tb
     host, (a, a_s, b, b_s) = _fp4_inputs(77, 400, 1536, int(kind), dev)
@@ -155,8 +156,8 @@ def _fp8_experts_pow2(e, h, inter, seed, dev):
 
 
 @pytest.mark.parametrize("fmt", ["fp8", "fp4"])
-@pytest.mark.parametrize("t,k,kind", [(9, 2, "auto"), (300, 8, "auto"), (300, 8, "17"), (300, 8, "11"),
-                                      (600, 8, "16")])
+@pytest.mark.parametrize("t,k,kind", [(9, 2, "auto"), (300, 8, "auto"), (300, 8, "17"), (300, 8, "20"),
+                                      (300, 8, "11"), (600, 8, "16")])
 def test_moe_pow2_matches_oracle(dev, monkeypatch, fmt, t, k, kind):
     """Routed experts under "ue8m0" with E8M0 weight scales: round_scale 2 (scales in
     the MFMA) against the per-expert oracle loop and the fold path (round_scale 1)."""

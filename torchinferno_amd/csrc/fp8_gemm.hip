@@ -677,6 +677,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 //  15  BM=128 BN=128, 8 waves 2x4 (wave 64x32),   32x32 MFMA            128     3   -- mid M
 //  16  BM=256 BN=256, 8 waves 2x4 (wave 128x64),  16x16 MFMA            128     2   -- prefill (scaled)
 //  17  BM=128 BN=256, 8 waves 2x4 (wave 64x64),   32x32 MFMA            128     3   -- MoE, ~128 rows/expert
+//  18  BM=192 BN=256, 8 waves 2x4 (wave 96x64),   32x32 MFMA            128     2   -- MoE, 129-192 rows/expert
+//  19  BM=192 BN=256, 8 waves 2x4 (wave 96x64),   16x16 MFMA            128     2   -- MoE (block scales)
+//  20  BM=128 BN=256, 8 waves 2x4 (wave 64x64),   16x16 MFMA            128     3   -- MoE (block scales)
 // The 8- and 16-wave kinds put two or four waves on each SIMD, which hides the
 // per-step barrier -> LDS read -> MFMA -> fold latency of one wave.
 // Block mode adds, after the ring, each wave's TM scale products (WGN * BM
@@ -728,6 +731,9 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
       case 15: launch_cfg<128, 128, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
       case 16: launch_cfg<256, 256, 128, 2, 4, 16, 2, SMODE, ODT>(p, x, stream); break;
       case 17: launch_cfg<128, 256, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
+      case 18: launch_cfg<192, 256, 128, 2, 4, 32, 2, SMODE, ODT>(p, x, stream); break;
+      case 19: launch_cfg<192, 256, 128, 2, 4, 16, 2, SMODE, ODT>(p, x, stream); break;
+      case 20: launch_cfg<128, 256, 128, 2, 4, 16, 3, SMODE, ODT>(p, x, stream); break;
       default: launch_cfg<256, 256, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
     }
   } else {
@@ -748,6 +754,9 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
       case 15: launch_cfg<128, 128, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
       case 16: launch_cfg<256, 256, 128, 2, 4, 16, 2, SMODE, ODT>(p, x, stream); break;
       case 17: launch_cfg<128, 256, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
+      case 18: launch_cfg<192, 256, 128, 2, 4, 32, 2, SMODE, ODT>(p, x, stream); break;
+      case 19: launch_cfg<192, 256, 128, 2, 4, 16, 2, SMODE, ODT>(p, x, stream); break;
+      case 20: launch_cfg<128, 256, 128, 2, 4, 16, 3, SMODE, ODT>(p, x, stream); break;
       case 14:
         if constexpr (SMODE == 0 || SMODE == 3) launch_cfg<256, 256, 128, 4, 4, 32, 2, SMODE, ODT>(p, x, stream);
         break;
@@ -756,8 +765,9 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
   }
 }
 
-const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256, 16, 16, 32, 64, 256, 128, 256, 128};
-const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128, 128, 128, 128, 256, 128, 128, 128, 256, 128, 256, 256};
+const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256, 16, 16, 32, 64, 256, 128, 256, 128, 192, 192, 128};
+const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128, 128, 128, 128, 256, 128, 128, 128, 256, 128, 256, 256,
+                            256, 256, 256};
 
 int env_int(const char* name, int dflt) {
   const char* e = getenv(name);
@@ -870,6 +880,12 @@ void launch_grouped_smode(int kind, const GemmArgs& x, int max_mtiles, hipStream
     case 13: launch_grouped_cfg<64, 128, 128, 2, 4, 16, 4, SMODE>(x, max_mtiles, stream); break;
     case 15: launch_grouped_cfg<128, 128, 128, 2, 4, 32, 3, SMODE>(x, max_mtiles, stream); break;
     case 17: launch_grouped_cfg<128, 256, 128, 2, 4, 32, 3, SMODE>(x, max_mtiles, stream); break;
+    case 18: launch_grouped_cfg<192, 256, 128, 2, 4, 32, 2, SMODE>(x, max_mtiles, stream); break;
+    case 19: launch_grouped_cfg<192, 256, 128, 2, 4, 16, 2, SMODE>(x, max_mtiles, stream); break;
+    case 20: launch_grouped_cfg<128, 256, 128, 2, 4, 16, 3, SMODE>(x, max_mtiles, stream); break;
+    case 14:
+      if constexpr (SMODE == 3) launch_grouped_cfg<256, 256, 128, 4, 4, 32, 2, SMODE>(x, max_mtiles, stream);
+      break;
     default: launch_grouped_cfg<16, 128, 128, 1, 4, 16, 6, SMODE>(x, max_mtiles, stream); break;
   }
 }

@@ -126,27 +126,34 @@ Plan make_plan(int T, int k, int E, int smode) {
   // Measured at the config-4 shapes: 8-wave 16- / 32-row tiles for few rows
   // per expert (T=64: avg 2; T=512: avg 16), 8-wave 128x256 at avg 128
   // (T=4096: one m-tile per expert and half the activation re-reads of
-  // 128x128; -20% FP8, -4% MXFP4), 8-wave 128x128 between.
-  (void)smode;
-  p.kind = avg <= 8 ? 11 : (avg <= 48 ? 12 : (avg <= 96 ? 15 : 17));
+  // 128x128; -20% FP8, -4% MXFP4), 8-wave 128x128 between.  At avg 128 the
+  // 16x16x128 form of the 128x256 tile (kind 20; 4-register partial sums)
+  // folds the block scales 1-2% faster than the 32x32x64 form (kind 17).
+  p.kind = avg <= 8 ? 11 : (avg <= 48 ? 12 : (avg <= 96 ? 15 : 20));
   const char* env = getenv("TI_ROCM_MOE_KIND");
   if (env && *env) {
     const int kk = atoi(env);
-    if (kk == 2 || kk == 5 || kk == 6 || kk == 9 || kk == 11 || kk == 12 || kk == 13 || kk == 15 || kk == 16 || kk == 17) p.kind = kk;
+    if (kk == 2 || kk == 5 || kk == 6 || kk == 9 || kk == 11 || kk == 12 || kk == 13 || kk == 15 || kk == 16 ||
+        kk == 17 || kk == 20)
+      p.kind = kk;
   }
   p.bm = fp8::grouped_bm(p.kind);
   p.max_tiles = (int)(R / p.bm + E + 1);
-  // Two tiers with the 128-row tile: an expert's rows go to 256-row tiles,
+  // Two tiers with the 128-row tile: an expert's rows go to 192-row tiles,
   // and a remainder of at most 128 rows to one 128-row tile.  An expert with
-  // 129-256 rows then streams its weights once (one 256-row tile) instead of
-  // once per 128-row tile.
+  // 129-192 rows then streams its weights once (one 192-row tile) instead of
+  // once per 128-row tile.  At T=4096 the rows per expert cluster around 128
+  // (sd ~11), so the second tier is mostly 129-160 rows: 192-row tiles
+  // (kind 19, 16x16x128 MFMAs) waste a third of the MFMA work of 256-row ones
+  // (kind 16) and measured 4-8% faster over the whole MoE.
   p.kind2 = -1;
   p.bm2 = 0;
   p.max_tiles2 = 0;
-  if (p.kind == 17) {
+  if (p.kind == 17 || p.kind == 20) {
     const char* e2 = getenv("TI_ROCM_MOE_KIND2");
-    p.kind2 = (e2 && *e2) ? atoi(e2) : 16;
-    if (p.kind2 != 9 && p.kind2 != 16) p.kind2 = -1;
+    p.kind2 = (e2 && *e2) ? atoi(e2) : 19;
+    if (p.kind2 != 9 && p.kind2 != 16 && p.kind2 != 18 && p.kind2 != 19 && !(p.kind2 == 14 && smode == 3))
+      p.kind2 = -1;
   }
   if (p.kind2 >= 0) {
     p.bm2 = fp8::grouped_bm(p.kind2);
@@ -465,10 +472,13 @@ static bool moe_shape_ok(int T, int k, int E, int H, int I) {
 
 extern "C" size_t ti_fp8_moe_workspace_bytes(int T, int k, int E, int H, int I) {
   if (!moe_shape_ok(T, k, E, H, I) || T == 0) return 0;
-  // One size serves both weight formats (their plans may pick different tiles).
-  const size_t b1 = carve(nullptr, T, k, E, H, I, make_plan(T, k, E, 1)).bytes;
-  const size_t b2 = carve(nullptr, T, k, E, H, I, make_plan(T, k, E, 2)).bytes;
-  return b1 > b2 ? b1 : b2;
+  // One size serves every weight and scale format (their plans may pick different tiles).
+  size_t b = 0;
+  for (int smode = 1; smode <= 4; ++smode) {
+    const size_t bs = carve(nullptr, T, k, E, H, I, make_plan(T, k, E, smode)).bytes;
+    b = bs > b ? bs : b;
+  }
+  return b;
 }
 
 // Routed experts, shared by the block-FP8 (smode 1: e4m3 weights, 128x128
