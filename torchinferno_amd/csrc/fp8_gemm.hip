@@ -264,9 +264,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
       dstep[u] = x.sa_layout ? M * 4 : 4;
       dper128[u] = true;
     } else if constexpr (BLK) {
-      // Only the tile's BN/128 column blocks are read; the other lanes repeat
-      // the last one (one cache line per step instead of 64).
-      const int nb = min(n0 / 128 + min(lane, (BN + 127) / 128 - 1), (N + 127) / 128 - 1);
+      // Only the column blocks the tile overlaps are read (a BN that is not a
+      // multiple of 128 may start inside a block and overlap one more); the
+      // other lanes repeat the last one (one cache line per step instead of 64).
+      constexpr int NBLK = (BN + 127) / 128 + (BN % 128 != 0);
+      const int nb = min(n0 / 128 + min(lane, NBLK - 1), (N + 127) / 128 - 1);
       dsrc[u] = (const uint8_t*)(sbmat + (long)nb * KB);
       dlds[u] = (uint32_t)(A_BYTES + B_BYTES + NI_SA * 256);
       dwide[u] = false;
@@ -374,7 +376,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
       int ea[FM], ebv = 127;
       if constexpr (SMODE == 3) {
         const float* sS = (const float*)(st + A_BYTES + B_BYTES);
-        ebv = e8m0_of(sS[NI_SA * 64 + (wn * TN) / 128]);
+        ebv = e8m0_of(sS[NI_SA * 64 + (n0 % 128 + wn * TN) / 128]);
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm) ea[fm] = e8m0_of(sS[wm * TM + fm * MF + lane % MF]);
       }
@@ -464,7 +466,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
       }
     } else {
       const float* sS = (const float*)(st + A_BYTES + B_BYTES);
-      const float sbv = sS[NI_SA * 64 + (wn * TN) / 128];
+      const float sbv = sS[NI_SA * 64 + (n0 % 128 + wn * TN) / 128];  // the wave's column block
       // LDS_PROD: the wave's TM row scales times its column block's scale,
       // one product per lane, through the wave's own LDS slot (a wave's LDS
       // accesses complete in order, so its reads below see its writes).
@@ -680,6 +682,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 //  18  BM=192 BN=256, 8 waves 2x4 (wave 96x64),   32x32 MFMA            128     2   -- MoE, 129-192 rows/expert
 //  19  BM=192 BN=256, 8 waves 2x4 (wave 96x64),   16x16 MFMA            128     2   -- MoE (block scales)
 //  20  BM=128 BN=256, 8 waves 2x4 (wave 64x64),   16x16 MFMA            128     3   -- MoE (block scales)
+//  21  BM=64  BN=224, 7 waves 1x7 (wave 64x32),   32x32 MFMA            128     4   -- small M, N = 7 * 2^k
 // The 8- and 16-wave kinds put two or four waves on each SIMD, which hides the
 // per-step barrier -> LDS read -> MFMA -> fold latency of one wave.
 // Block mode adds, after the ring, each wave's TM scale products (WGN * BM
@@ -757,6 +760,7 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
       case 18: launch_cfg<192, 256, 128, 2, 4, 32, 2, SMODE, ODT>(p, x, stream); break;
       case 19: launch_cfg<192, 256, 128, 2, 4, 16, 2, SMODE, ODT>(p, x, stream); break;
       case 20: launch_cfg<128, 256, 128, 2, 4, 16, 3, SMODE, ODT>(p, x, stream); break;
+      case 21: launch_cfg<64, 224, 128, 1, 7, 32, 4, SMODE, ODT>(p, x, stream); break;
       case 14:
         if constexpr (SMODE == 0 || SMODE == 3) launch_cfg<256, 256, 128, 4, 4, 32, 2, SMODE, ODT>(p, x, stream);
         break;
@@ -765,9 +769,9 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
   }
 }
 
-const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256, 16, 16, 32, 64, 256, 128, 256, 128, 192, 192, 128};
+const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256, 16, 16, 32, 64, 256, 128, 256, 128, 192, 192, 128, 64};
 const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128, 128, 128, 128, 256, 128, 128, 128, 256, 128, 256, 256,
-                            256, 256, 256};
+                            256, 256, 256, 224};
 
 int env_int(const char* name, int dflt) {
   const char* e = getenv(name);
@@ -790,6 +794,8 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   // tile that still gives every CU a workgroup (256x256, then 256x128 from 144
   // tiles -- 128 with block or MXFP4 scales -- then 128x128).
   auto tiles = [&](int bm, int bn) { return (long)cdiv(M, bm) * cdiv(N, bn); };
+  // fraction of the last wave of 256 workgroups that is occupied, over all waves
+  auto fill = [](long t) { return (double)t / (double)(cdiv((int)t, 256) * 256); };
   int splits = 1;
   if (M <= 4 && (smode != 0 || tiles(16, 256) >= 128)) {
     // 4-wave 16x256 tiles; split over K below 128 column tiles: up to 4 ways,
@@ -807,6 +813,12 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
     p.kind = 11;
     const long t = tiles(16, 128);
     if (t < 128) splits = t * 4 <= 256 ? 4 : 2;
+  } else if (smode == 0 && M <= 64 && fill(tiles(64, 224)) > fill(tiles(M <= 32 ? 32 : 64, 128)) + 0.05 &&
+             tiles(64, 224) >= 192) {
+    // 7-wave 64x224 tiles where N = 7 * 2^k gives a whole number of waves of
+    // 256 workgroups and 128-column tiles do not (config-2 gate_up, N=57344:
+    // 256 tiles instead of 448, M=64 94 -> 88 us, M=32 87 -> 83 us).
+    p.kind = 21;
   } else if (M <= 32) {
     p.kind = 12;
     splits = tiles(32, 128) >= 128 ? 1 : 2;
@@ -853,7 +865,8 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   }
   p.kind = env_int("TI_ROCM_FP8_KIND", p.kind);
   if (p.kind < 0 || p.kind >= kNumKinds) p.kind = 1;
-  if (smode == 2 && (p.kind == 0 || p.kind == 4 || p.kind == 7 || p.kind == 8)) p.kind = 1;  // not built for e2m1
+  if (smode == 2 && (p.kind == 0 || p.kind == 4 || p.kind == 7 || p.kind == 8 || p.kind == 21))
+    p.kind = 1;  // not built for e2m1
   if (smode != 0 && p.kind == 14) p.kind = 1;  // per-token only (the scaled folds would spill)
   p.group_m = env_int("TI_ROCM_FP8_GROUP_M", 4);
   if (p.group_m < 1) p.group_m = 1;
