@@ -683,6 +683,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 //  19  BM=192 BN=256, 8 waves 2x4 (wave 96x64),   16x16 MFMA            128     2   -- MoE (block scales)
 //  20  BM=128 BN=256, 8 waves 2x4 (wave 64x64),   16x16 MFMA            128     3   -- MoE (block scales)
 //  21  BM=64  BN=224, 7 waves 1x7 (wave 64x32),   32x32 MFMA            128     4   -- small M, N = 7 * 2^k
+//  22  BM=256 BN=96, 12 waves 4x3 (wave 64x32),   32x32 MFMA            128     3   -- mid M (per-token)
 // The 8- and 16-wave kinds put two or four waves on each SIMD, which hides the
 // per-step barrier -> LDS read -> MFMA -> fold latency of one wave.
 // Block mode adds, after the ring, each wave's TM scale products (WGN * BM
@@ -761,6 +762,9 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
       case 19: launch_cfg<192, 256, 128, 2, 4, 16, 2, SMODE, ODT>(p, x, stream); break;
       case 20: launch_cfg<128, 256, 128, 2, 4, 16, 3, SMODE, ODT>(p, x, stream); break;
       case 21: launch_cfg<64, 224, 128, 1, 7, 32, 4, SMODE, ODT>(p, x, stream); break;
+      case 22:  // the plan maps it to kind 9 in block mode (its fold would spill at 12 waves)
+        if constexpr (SMODE != 1) launch_cfg<256, 96, 128, 4, 3, 32, 3, SMODE, ODT>(p, x, stream);
+        break;
       case 14:
         if constexpr (SMODE == 0 || SMODE == 3) launch_cfg<256, 256, 128, 4, 4, 32, 2, SMODE, ODT>(p, x, stream);
         break;
@@ -769,9 +773,9 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
   }
 }
 
-const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256, 16, 16, 32, 64, 256, 128, 256, 128, 192, 192, 128, 64};
+const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256, 16, 16, 32, 64, 256, 128, 256, 128, 192, 192, 128, 64, 256};
 const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128, 128, 128, 128, 256, 128, 128, 128, 256, 128, 256, 256,
-                            256, 256, 256, 224};
+                            256, 256, 256, 224, 96};
 
 int env_int(const char* name, int dflt) {
   const char* e = getenv(name);
@@ -850,6 +854,11 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
     // partial sums leave room to fold one tile while the next one's MFMAs run
     // (2-4% over the 32x32x64 form).
     p.kind = smode == 0 ? 14 : 16;
+  } else if (smode == 0 && tiles(256, 128) >= 144 && tiles(256, 96) <= 256 &&
+             fill(tiles(256, 96)) > fill(tiles(256, 128)) + 0.1) {
+    // 12-wave 256x96 tiles when they fill the 256 CUs better than 256x128
+    // ones (config-2 qkv M=512, N=10240: 214 instead of 160 tiles, 74 -> 60 us)
+    p.kind = 22;
   } else if (tiles(256, 128) >= (smode >= 1 ? 128 : 144)) {
     p.kind = 9;
   } else if (smode == 0 && tiles(256, 128) >= 64) {
@@ -865,9 +874,10 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   }
   p.kind = env_int("TI_ROCM_FP8_KIND", p.kind);
   if (p.kind < 0 || p.kind >= kNumKinds) p.kind = 1;
-  if (smode == 2 && (p.kind == 0 || p.kind == 4 || p.kind == 7 || p.kind == 8 || p.kind == 21))
+  if (smode == 2 && (p.kind == 0 || p.kind == 4 || p.kind == 7 || p.kind == 8 || p.kind == 21 || p.kind == 22))
     p.kind = 1;  // not built for e2m1
   if (smode != 0 && p.kind == 14) p.kind = 1;  // per-token only (the scaled folds would spill)
+  if (smode == 1 && p.kind == 22) p.kind = 9;
   p.group_m = env_int("TI_ROCM_FP8_GROUP_M", 4);
   if (p.group_m < 1) p.group_m = 1;
   p.tiles_m = cdiv(M, kBM[p.kind]);
