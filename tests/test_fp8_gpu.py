@@ -314,7 +314,7 @@ def test_rowcol_ragged(dev, m, n):
     assert err <= TOL, err
 
 
-@pytest.mark.parametrize("kind", range(23))
+@pytest.mark.parametrize("kind", range(24))
 @pytest.mark.parametrize("mode", ["rowcol", "block"])
 def test_every_tile_kind(dev, monkeypatch, kind, mode):
     """Each tile configuration, forced, on a ragged problem, with and without split-K."""
@@ -502,7 +502,7 @@ def test_tiled_weight_gemm_equals_row_layout(dev, m):
     assert err <= TOL
 
 
-@pytest.mark.parametrize("kind", [k for k in range(23) if k not in (0, 7, 8)])
+@pytest.mark.parametrize("kind", [k for k in range(24) if k not in (0, 7, 8)])
 def test_tiled_weight_every_kind(dev, monkeypatch, kind):
     """Every 128-K-step tile kind (the 64-K-step kinds run kind 1 on tiled weights),
     with and without split-K, on a ragged M: tiled equals row layout."""

@@ -64,7 +64,7 @@ def _check_block(y, a, a_s, codes, s):
     return elementwise_ratio(y.float().cpu().numpy(), ref, ref_abs)
 
 
-@pytest.mark.parametrize("kind", range(23))
+@pytest.mark.parametrize("kind", range(24))
 def test_block_pow2_every_kind(dev, monkeypatch, kind):
     from torchinferno_amd.kernels import block_fp8 as tb
     a, a_s, b, b_s, codes, s = _block_problem(200, 1280, 400, 50 + kind, dev)

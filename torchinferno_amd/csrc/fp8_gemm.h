@@ -6,7 +6,7 @@
 namespace ti {
 namespace fp8 {
 
-constexpr int kNumKinds = 23;
+constexpr int kNumKinds = 24;
 
 struct GemmArgs {
   const uint8_t* a;   // [M, K] e4m3

@@ -684,6 +684,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 //  20  BM=128 BN=256, 8 waves 2x4 (wave 64x64),   16x16 MFMA            128     3   -- MoE (block scales)
 //  21  BM=64  BN=224, 7 waves 1x7 (wave 64x32),   32x32 MFMA            128     4   -- small M, N = 7 * 2^k
 //  22  BM=256 BN=96, 12 waves 4x3 (wave 64x32),   32x32 MFMA            128     3   -- mid M (per-token)
+//  23  BM=16  BN=144, 9 waves 1x9 (wave 16x16),   16x16 MFMA            128     6   -- decode, N = 9 * 2^k
 // The 8- and 16-wave kinds put two or four waves on each SIMD, which hides the
 // per-step barrier -> LDS read -> MFMA -> fold latency of one wave.
 // Block mode adds, after the ring, each wave's TM scale products (WGN * BM
@@ -765,6 +766,7 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
       case 22:  // the plan maps it to kind 9 in block mode (its fold would spill at 12 waves)
         if constexpr (SMODE != 1) launch_cfg<256, 96, 128, 4, 3, 32, 3, SMODE, ODT>(p, x, stream);
         break;
+      case 23: launch_cfg<16, 144, 128, 1, 9, 16, 6, SMODE, ODT>(p, x, stream); break;
       case 14:
         if constexpr (SMODE == 0 || SMODE == 3) launch_cfg<256, 256, 128, 4, 4, 32, 2, SMODE, ODT>(p, x, stream);
         break;
@@ -773,9 +775,9 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
   }
 }
 
-const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256, 16, 16, 32, 64, 256, 128, 256, 128, 192, 192, 128, 64, 256};
+const int kBM[kNumKinds] = {256, 256, 128, 16, 32, 64, 16, 128, 256, 256, 16, 16, 32, 64, 256, 128, 256, 128, 192, 192, 128, 64, 256, 16};
 const int kBN[kNumKinds] = {256, 256, 128, 256, 256, 128, 128, 128, 128, 128, 256, 128, 128, 128, 256, 128, 256, 256,
-                            256, 256, 256, 224, 96};
+                            256, 256, 256, 224, 96, 144};
 
 int env_int(const char* name, int dflt) {
   const char* e = getenv(name);
@@ -817,6 +819,12 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
     p.kind = 11;
     const long t = tiles(16, 128);
     if (t < 128) splits = t * 4 <= 256 ? 4 : 2;
+    else if (smode != 2 && t < 256 && 2 * tiles(16, 144) <= 256 && fill(2 * tiles(16, 144)) > fill(t) + 0.1) {
+      // 9-wave 16x144 tiles split in two where N = 9 * 2^k (config-3 a,
+      // N=18432: 256 workgroups instead of 144; 27 -> 23 us)
+      p.kind = 23;
+      splits = 2;
+    }
   } else if (smode == 0 && M <= 64 && fill(tiles(64, 224)) > fill(tiles(M <= 32 ? 32 : 64, 128)) + 0.05 &&
              tiles(64, 224) >= 192) {
     // 7-wave 64x224 tiles where N = 7 * 2^k gives a whole number of waves of
@@ -874,7 +882,7 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   }
   p.kind = env_int("TI_ROCM_FP8_KIND", p.kind);
   if (p.kind < 0 || p.kind >= kNumKinds) p.kind = 1;
-  if (smode == 2 && (p.kind == 0 || p.kind == 4 || p.kind == 7 || p.kind == 8 || p.kind == 21 || p.kind == 22))
+  if (smode == 2 && (p.kind == 0 || p.kind == 4 || p.kind == 7 || p.kind == 8 || p.kind >= 21))
     p.kind = 1;  // not built for e2m1
   if (smode != 0 && p.kind == 14) p.kind = 1;  // per-token only (the scaled folds would spill)
   if (smode == 1 && p.kind == 22) p.kind = 9;
