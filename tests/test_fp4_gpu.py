@@ -46,7 +46,7 @@ def test_fp4_gemm_matches_oracle(dev, m, n, k):
     assert _rel_err(y.float().cpu().numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("kind", ["1", "2", "3", "5", "6", "9", "10", "11", "12", "13", "15", "16", "17", "18",
+@pytest.mark.parametrize("kind", ["1", "2", "3", "5", "6", "9", "10", "11", "12", "13", "15", "16", "17", "18", "23",
                                   "19", "20"])
 @pytest.mark.parametrize("splits", ["1", "3"])
 def test_fp4_gemm_every_kind(dev, monkeypatch, kind, splits):

@@ -123,7 +123,7 @@ def _fp4_inputs(m, n, k, seed, dev):
     return (a, a_s, b, b_s), t
 
 
-@pytest.mark.parametrize("kind", ["1", "2", "3", "5", "6", "9", "10", "11", "12", "13", "15", "16", "17", "18",
+@pytest.mark.parametrize("kind", ["1", "2", "3", "5", "6", "9", "10", "11", "12", "13", "15", "16", "17", "18", "23",
                                   "19", "20"])
 def test_fp4_pow2_every_kind(dev, monkeypatch, kind):
     from torchinferno_amd.kernels import block_fp8 as tb

@@ -739,6 +739,7 @@ void launch_kind(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
       case 18: launch_cfg<192, 256, 128, 2, 4, 32, 2, SMODE, ODT>(p, x, stream); break;
       case 19: launch_cfg<192, 256, 128, 2, 4, 16, 2, SMODE, ODT>(p, x, stream); break;
       case 20: launch_cfg<128, 256, 128, 2, 4, 16, 3, SMODE, ODT>(p, x, stream); break;
+      case 23: launch_cfg<16, 144, 128, 1, 9, 16, 6, SMODE, ODT>(p, x, stream); break;
       default: launch_cfg<256, 256, 128, 2, 4, 32, 3, SMODE, ODT>(p, x, stream); break;
     }
   } else {
@@ -819,9 +820,10 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
     p.kind = 11;
     const long t = tiles(16, 128);
     if (t < 128) splits = t * 4 <= 256 ? 4 : 2;
-    else if (smode != 2 && t < 256 && 2 * tiles(16, 144) <= 256 && fill(2 * tiles(16, 144)) > fill(t) + 0.1) {
+    else if (t < 256 && 2 * tiles(16, 144) <= 256 && fill(2 * tiles(16, 144)) > fill(t) + 0.1) {
       // 9-wave 16x144 tiles split in two where N = 9 * 2^k (config-3 a,
-      // N=18432: 256 workgroups instead of 144; 27 -> 23 us)
+      // N=18432: 256 workgroups instead of 144; block FP8 27 -> 23 us, MXFP4
+      // 22.4 -> 15.7 us)
       p.kind = 23;
       splits = 2;
     }
@@ -882,7 +884,7 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
   }
   p.kind = env_int("TI_ROCM_FP8_KIND", p.kind);
   if (p.kind < 0 || p.kind >= kNumKinds) p.kind = 1;
-  if (smode == 2 && (p.kind == 0 || p.kind == 4 || p.kind == 7 || p.kind == 8 || p.kind >= 21))
+  if (smode == 2 && (p.kind == 0 || p.kind == 4 || p.kind == 7 || p.kind == 8 || p.kind == 21 || p.kind == 22))
     p.kind = 1;  // not built for e2m1
   if (smode != 0 && p.kind == 14) p.kind = 1;  // per-token only (the scaled folds would spill)
   if (smode == 1 && p.kind == 22) p.kind = 9;
