@@ -33,7 +33,8 @@ def _rel_err(y, ref):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m,k", [(1, 128), (7, 136), (64, 8192), (33, 28672)])
+@pytest.mark.parametrize("m,k", [(1, 128), (7, 136), (64, 8192), (33, 28672), (512, 28672), (600, 20000),
+                                 (1024, 4096)])
 def test_per_token_quant_bit_exact(dev, dtype, m, k):
     from torchinferno_amd.kernels import fp8 as tf8
     g = torch.Generator().manual_seed(m * 7 + k)
@@ -42,6 +43,62 @@ def test_per_token_quant_bit_exact(dev, dtype, m, k):
     oq, os_ = ofp8.quantize_activation_per_token(x.float().numpy())
     assert np.array_equal(_codes(xq), oq)
     assert np.array_equal(xs.cpu().numpy().view(np.uint32), os_.view(np.uint32))
+
+
+@pytest.mark.parametrize("m", [1, 300])
+@pytest.mark.parametrize("amax", [672.0, 784.0, 840.0, 448.0 * 1.3, 448.0 * 0.7])
+def test_per_token_quant_e4m3_midpoints(dev, m, amax):
+    """Quotients on and next to e4m3 rounding midpoints, where a reciprocal product
+    and the IEEE quotient can round to different codes: every e4m3 midpoint times
+    the row scale, and its bf16 neighbours.  With amax 672 / 784 / 840 the scale is
+    1.5 / 1.75 / 1.875, every such product is exact in bf16 and every quotient an
+    exact tie; for 1.75 and 1.875, fl(x * fl(1/s)) lands one ulp above many of
+    those ties, so a plain reciprocal product would round them up."""
+    from torchinferno_amd.kernels import fp8 as tf8
+    codes = np.arange(1, 0x7E, dtype=np.uint8)
+    vals = ofp8.e4m3_decode(codes).astype(np.float64)
+    mids = (vals[:-1] + vals[1:]) / 2
+    amax = float(torch.tensor(amax).to(torch.bfloat16))
+    sc = np.float32(np.float32(amax) / np.float32(448.0))
+    base = torch.tensor(np.concatenate([mids, -mids]) * float(sc), dtype=torch.float32).to(torch.bfloat16)
+    bits = base.view(torch.int16)
+    row = torch.cat([base, (bits + 1).view(torch.bfloat16), (bits - 1).view(torch.bfloat16)])
+    row = torch.cat([row, torch.tensor([amax], dtype=torch.bfloat16)])
+    k = -(-row.numel() // 8) * 8
+    x = torch.zeros((m, k), dtype=torch.bfloat16)
+    x[:, :row.numel()] = row
+    assert float(x.abs().max()) == float(torch.tensor(amax).to(torch.bfloat16))
+    xq, xs = tf8.quantize_activation_fp8_per_token(x.to(dev))
+    oq, os_ = ofp8.quantize_activation_per_token(x.float().numpy())
+    assert np.array_equal(xs.cpu().numpy().view(np.uint32), os_.view(np.uint32))
+    assert np.array_equal(_codes(xq), oq)
+
+
+@pytest.mark.parametrize("round_scale", [False, True])
+@pytest.mark.parametrize("amax", [672.0, 784.0, 840.0, 448.0 * 1.3])
+def test_block_act_quant_e4m3_midpoints(dev, round_scale, amax):
+    """The 1x128 quant on quotients at and next to e4m3 midpoints (as the per-token
+    test above): each 128-wide block holds its amax and 127 such values."""
+    from torchinferno_amd.kernels import block_fp8 as tb
+    codes = np.arange(1, 0x7E, dtype=np.uint8)
+    vals = ofp8.e4m3_decode(codes).astype(np.float64)
+    mids = (vals[:-1] + vals[1:]) / 2
+    amax = float(torch.tensor(amax).to(torch.bfloat16))
+    sc = np.float32(np.float32(amax) * np.float32(1.0 / 448.0))
+    base = torch.tensor(np.concatenate([mids, -mids]) * float(sc), dtype=torch.float32).to(torch.bfloat16)
+    bits = base.view(torch.int16)
+    vals_all = torch.cat([base, (bits + 1).view(torch.bfloat16), (bits - 1).view(torch.bfloat16)])
+    nblk = -(-vals_all.numel() // 127)
+    x = torch.zeros((nblk, 128), dtype=torch.bfloat16)
+    flat = torch.zeros(nblk * 127, dtype=torch.bfloat16)
+    flat[:vals_all.numel()] = vals_all
+    x[:, :127] = flat.view(nblk, 127)
+    x[:, 127] = amax
+    x = x.reshape(1, -1).repeat(3, 1)
+    xq, xs = tb.act_quant(x.to(dev), 128, "ue8m0" if round_scale else None)
+    oq, os_ = ofp8.act_quant_block(x.float().numpy(), round_scale=round_scale)
+    assert np.array_equal(xs.cpu().numpy().view(np.uint32), os_.view(np.uint32))
+    assert np.array_equal(_codes(xq), oq)
 
 
 def test_per_token_quant_zero_row_uses_eps(dev):

@@ -45,6 +45,22 @@ __device__ __forceinline__ uint2 e4m3_pack8_hw(const float (&y)[8]) {
                     e4m3_encode2_hw(y[4], y[5]) | (e4m3_encode2_hw(y[6], y[7]) << 16));
 }
 
+// x / sc as the e4m3 conversion sees it, without a division per element.  r is
+// the correctly rounded 1/sc.  q = fl(x * r) lies within one fp32 ulp of the
+// correctly rounded quotient fl(x / sc), so both round to the same e4m3 value
+// unless they sit within a few ulps of an e4m3 rounding midpoint (low 20
+// mantissa bits near 0x80000), below the e4m3 normal range (2^-6, where the
+// rounding position moves), or near the top of the range (447 and above); there
+// the quotient itself is returned.  The e4m3 codes are therefore those of the
+// IEEE quotient; the returned float itself may differ from it by an ulp.
+__device__ __forceinline__ float quot_for_e4m3(float x, float sc, float r) {
+  const float q = x * r;
+  const float a = fabsf(q);
+  const uint32_t lo = __float_as_uint(q) & 0xFFFFFu;
+  const bool clear = a >= 0.015625f && a < 447.0f && (lo - 0x7FFF8u) > 0x10u;  // |lo - 0x80000| > 8
+  return clear ? q : x / sc;
+}
+
 template <int DT>
 __device__ __forceinline__ float act_to_f32(uint16_t h) {
   if constexpr (DT == TI_DTYPE_F16) return f16_bits_to_f32(h);

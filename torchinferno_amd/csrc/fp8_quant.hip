@@ -12,9 +12,11 @@
 //   tensor scale (static or precomputed dynamic scale):
 //     q = e4m3(x * inv_scale)  -- fp8.py:43-51 (_scale_cast_fp8)
 //
-// All arithmetic is fp32 with IEEE division (no reciprocal approximation), and
-// the cast is round-to-nearest-even, so codes and scales are bit-identical to
-// the same formulas evaluated by torch on the host.
+// All arithmetic is fp32.  Scales come from IEEE division; the per-element
+// quotients x / s reach the e4m3 cast as a product with 1/s where that provably
+// rounds to the same code, else as the quotient (quot_for_e4m3).  The cast is
+// round-to-nearest-even, so codes and scales are bit-identical to the same
+// formulas evaluated by torch on the host.
 #include <type_traits>
 
 #include "fp8_common.h"
@@ -85,6 +87,56 @@ __global__ __launch_bounds__(256) void quant_per_token_kernel(const uint16_t* __
   }
 }
 
+// The same per-token quant for one workgroup per row with the row held in
+// registers between the max and the quantization (NI 8-element loads per
+// thread, K <= NI * 2048): x is read from memory once.  Codes as above (the
+// quotient through quot_for_e4m3).
+template <int DT, bool RECIP, int NI>
+__global__ __launch_bounds__(256) void quant_per_token_reg_kernel(const uint16_t* __restrict__ x, int K,
+                                                                  uint8_t* __restrict__ q,
+                                                                  float* __restrict__ s, float eps) {
+  __shared__ float red[4];
+  const long row = blockIdx.x;
+  const uint16_t* xr = x + row * K;
+  uint4 v[NI];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int i = (j * 256 + (int)threadIdx.x) * 8;
+    v[j] = i < K ? *(const uint4*)(xr + i) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      amax = fmaxf(amax, fmaxf(fabsf(act_to_f32<DT>((uint16_t)(w[e] & 0xFFFFu))),
+                               fabsf(act_to_f32<DT>((uint16_t)(w[e] >> 16)))));
+  }
+  amax = wave_max(amax);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float sc = fmaxf(RECIP ? amax * (1.0f / kE4M3Max) : amax / kE4M3Max, eps);
+  const float r = 1.0f / sc;
+  if (threadIdx.x == 0) s[row] = sc;
+  uint8_t* qr = q + row * K;
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int i = (j * 256 + (int)threadIdx.x) * 8;
+    if (i < K) {
+      const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+      float y[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        y[2 * e] = quot_for_e4m3(act_to_f32<DT>((uint16_t)(w[e] & 0xFFFFu)), sc, r);
+        y[2 * e + 1] = quot_for_e4m3(act_to_f32<DT>((uint16_t)(w[e] >> 16)), sc, r);
+      }
+      *(uint2*)(qr + i) = e4m3_pack8_hw(y);
+    }
+  }
+}
+
 // One wave per (row, 128-column block): 2 elements per lane.
 template <int DT, bool POW2>
 __global__ __launch_bounds__(256) void quant_block_kernel(const uint16_t* __restrict__ x, int M, int K,
@@ -151,9 +203,12 @@ __global__ __launch_bounds__(256) void quant_block_wide_kernel(const uint16_t* _
   } else {
     sc = amax * inv_max;
   }
+  // power-of-two scales: the product with the exact reciprocal is the quotient
+  const float r = 1.0f / sc;
   float y[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = fminf(fmaxf(f[e] / sc, -kE4M3Max), kE4M3Max);
+  for (int e = 0; e < 8; ++e)
+    y[e] = fminf(fmaxf(POW2 ? f[e] * r : quot_for_e4m3(f[e], sc, r), -kE4M3Max), kE4M3Max);
   if (on) {
     *(uint2*)(q + off) = e4m3_pack8_hw(y);
     if ((lane & 15) == 0) s[s_layout ? (long)kb * M + row : row * KB + kb] = sc;
@@ -227,6 +282,7 @@ template <int V>
 __device__ __forceinline__ void row_quant_store(float (&v)[V][8], float amax, int n, uint8_t* __restrict__ qr,
                                                 float* __restrict__ s_out) {
   const float sc = fmaxf(amax / kE4M3Max, 1e-10f);
+  const float r = 1.0f / sc;
   if (threadIdx.x == 0) *s_out = sc;
 #pragma unroll
   for (int j = 0; j < V; ++j) {
@@ -234,7 +290,7 @@ __device__ __forceinline__ void row_quant_store(float (&v)[V][8], float amax, in
     if (i < n) {
       float y[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) y[e] = v[j][e] / sc;  // |y| <= 448 by the choice of sc
+      for (int e = 0; e < 8; ++e) y[e] = quot_for_e4m3(v[j][e], sc, r);  // |y| <= 448 by the choice of sc
       *(uint2*)(qr + i) = e4m3_pack8_hw(y);
     }
   }
@@ -432,6 +488,31 @@ static int quant_rows(const char* who, bool recip, const void* x, int x_dtype, i
   if (M == 0) return TI_OK;
   // column chunks: about 512 workgroups in all, each at least 2048 elements
   const int chunks = std::max(1, std::min((511 + M) / M, K / 2048));
+  if (chunks == 1 && K <= 16 * 2048) {
+    // one workgroup per row, the row in registers (NI loads of 8 per thread)
+    const int ni = (K + 2047) / 2048;
+#define TI_QRR(DT, R, NI)                                                                                      \
+  hipLaunchKernelGGL((quant_per_token_reg_kernel<DT, R, NI>), dim3(M), dim3(256), 0, stream, (const uint16_t*)x, \
+                     K, xq, xs, eps)
+#define TI_QRN(DT, R)                                  \
+  do {                                                 \
+    if (ni <= 1) TI_QRR(DT, R, 1);                     \
+    else if (ni <= 2) TI_QRR(DT, R, 2);                \
+    else if (ni <= 4) TI_QRR(DT, R, 4);                \
+    else if (ni <= 8) TI_QRR(DT, R, 8);                \
+    else if (ni <= 12) TI_QRR(DT, R, 12);              \
+    else TI_QRR(DT, R, 16);                            \
+  } while (0)
+    if (x_dtype == TI_DTYPE_F16) {
+      if (recip) TI_QRN(TI_DTYPE_F16, true); else TI_QRN(TI_DTYPE_F16, false);
+    } else {
+      if (recip) TI_QRN(TI_DTYPE_BF16, true); else TI_QRN(TI_DTYPE_BF16, false);
+    }
+#undef TI_QRN
+#undef TI_QRR
+    TI_CHECK_LAUNCH(who);
+    return TI_OK;
+  }
 #define TI_QR(DT, R)                                                                                             \
   hipLaunchKernelGGL((quant_per_token_kernel<DT, R>), dim3(M, chunks), dim3(256), 0, stream, (const uint16_t*)x, K, \
                      xq, xs, eps)

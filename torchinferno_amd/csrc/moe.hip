@@ -380,9 +380,12 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t* __res
       const int e = (int)((bits >> 23) & 0xFF) - 127 + ((bits & 0x7FFFFFu) != 0 ? 1 : 0);
       sc = __uint_as_float((uint32_t)(e + 127) << 23);
     }
+    // x / sc: exact as a product for power-of-two scales, else quot_for_e4m3
+    const float r = 1.0f / sc;
     float y[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = fminf(fmaxf(h[i] / sc, -kE4M3Max), kE4M3Max);
+    for (int i = 0; i < 8; ++i)
+      y[i] = fminf(fmaxf(round_scale ? h[i] * r : fp8::quot_for_e4m3(h[i], sc, r), -kE4M3Max), kE4M3Max);
     if (on) {
       *(uint2*)(hq + p * I + c) = fp8::e4m3_pack8_hw(y);
       if ((lane & 15) == 0) hs[p * IB + blk] = sc;
