@@ -34,7 +34,7 @@ def _rel_err(y, ref):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m,k", [(1, 128), (7, 136), (64, 8192), (33, 28672), (512, 28672), (600, 20000),
-                                 (1024, 4096)])
+                                 (1024, 4096), (2048, 9000), (2100, 2056)])
 def test_per_token_quant_bit_exact(dev, dtype, m, k):
     from torchinferno_amd.kernels import fp8 as tf8
     g = torch.Generator().manual_seed(m * 7 + k)

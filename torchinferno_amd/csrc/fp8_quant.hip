@@ -486,8 +486,10 @@ static int quant_rows(const char* who, bool recip, const void* x, int x_dtype, i
   TI_CHECK_ARG(((uintptr_t)x & 15) == 0 && ((uintptr_t)xq & 7) == 0,
                "%s: input must be 16-byte and output 8-byte aligned", who);
   if (M == 0) return TI_OK;
-  // column chunks: about 512 workgroups in all, each at least 2048 elements
-  const int chunks = std::max(1, std::min((511 + M) / M, K / 2048));
+  // column chunks: about 2048 workgroups in all, each at least 2048 elements
+  // (measured: 512x28672 15.5 us on 4 chunks vs 19 us on one register-resident
+  // workgroup per row; from 2048 rows one workgroup per row is fastest)
+  const int chunks = std::max(1, std::min((2047 + M) / M, K / 2048));
   if (chunks == 1 && K <= 16 * 2048) {
     // one workgroup per row, the row in registers (NI loads of 8 per thread)
     const int ni = (K + 2047) / 2048;
