@@ -203,12 +203,18 @@ __global__ __launch_bounds__(256) void quant_block_wide_kernel(const uint16_t* _
   } else {
     sc = amax * inv_max;
   }
-  // power-of-two scales: the product with the exact reciprocal is the quotient
-  const float r = 1.0f / sc;
+  // Power-of-two scales: the product with the exact reciprocal is the quotient.
+  // (With other scales quot_for_e4m3 measured slower here than the division:
+  // eight quotients per lane do not repay the reciprocal.)
   float y[8];
+  if constexpr (POW2) {
+    const float r = 1.0f / sc;
 #pragma unroll
-  for (int e = 0; e < 8; ++e)
-    y[e] = fminf(fmaxf(POW2 ? f[e] * r : quot_for_e4m3(f[e], sc, r), -kE4M3Max), kE4M3Max);
+    for (int e = 0; e < 8; ++e) y[e] = fminf(fmaxf(f[e] * r, -kE4M3Max), kE4M3Max);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = fminf(fmaxf(f[e] / sc, -kE4M3Max), kE4M3Max);
+  }
   if (on) {
     *(uint2*)(q + off) = e4m3_pack8_hw(y);
     if ((lane & 15) == 0) s[s_layout ? (long)kb * M + row : row * KB + kb] = sc;
