@@ -101,7 +101,7 @@ def test_router_options(dev):
 
 
 @pytest.mark.parametrize("t,k", [(1, 1), (7, 2), (64, 4), (300, 8)])
-@pytest.mark.parametrize("kind", ["auto", "2", "5", "6", "9", "11", "12", "13", "15", "17", "20"])
+@pytest.mark.parametrize("kind", ["auto", "2", "3", "4", "5", "6", "9", "10", "11", "12", "13", "15", "17", "20"])
 def test_moe_small_matches_oracle(dev, monkeypatch, t, k, kind):
     from torchinferno_amd.kernels import moe as tmoe
     print(f"[moe] small T={t} k={k} kind={kind}", flush=True)

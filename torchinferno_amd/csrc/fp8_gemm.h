@@ -48,7 +48,7 @@ size_t gemm_ticket_bytes(const GemmPlan& p);
 void launch_gemm(const GemmPlan& p, int smode, int odt, const GemmArgs& x, hipStream_t stream);
 
 // Grouped block-scaled GEMM (bf16 out) over a device m-tile table; kind is one
-// of 2, 5, 9, 11, 12, 13, 15-20, and 14 with power-of-two block scales
+// of 2-5, 9-13, 15-20, and 14 with power-of-two block scales
 // (the tile configurations of fp8_gemm.hip).
 int grouped_bm(int kind);
 int grouped_bn(int kind);

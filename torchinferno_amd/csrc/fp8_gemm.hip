@@ -909,6 +909,9 @@ void launch_grouped_smode(int kind, const GemmArgs& x, int max_mtiles, hipStream
     case 9: launch_grouped_cfg<256, 128, 128, 4, 2, 32, 3, SMODE>(x, max_mtiles, stream); break;
     case 16: launch_grouped_cfg<256, 256, 128, 2, 4, 16, 2, SMODE>(x, max_mtiles, stream); break;
     case 11: launch_grouped_cfg<16, 128, 128, 1, 8, 16, 6, SMODE>(x, max_mtiles, stream); break;
+    case 3: launch_grouped_cfg<16, 256, 128, 1, 4, 16, 4, SMODE>(x, max_mtiles, stream); break;
+    case 4: launch_grouped_cfg<32, 256, 128, 1, 4, 16, 4, SMODE>(x, max_mtiles, stream); break;
+    case 10: launch_grouped_cfg<16, 256, 128, 1, 8, 16, 4, SMODE>(x, max_mtiles, stream); break;
     case 12: launch_grouped_cfg<32, 128, 128, 1, 8, 16, 6, SMODE>(x, max_mtiles, stream); break;
     case 13: launch_grouped_cfg<64, 128, 128, 2, 4, 16, 4, SMODE>(x, max_mtiles, stream); break;
     case 15: launch_grouped_cfg<128, 128, 128, 2, 4, 32, 3, SMODE>(x, max_mtiles, stream); break;

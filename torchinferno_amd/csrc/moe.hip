@@ -123,17 +123,21 @@ Plan make_plan(int T, int k, int E, int smode) {
   const long R = (long)T * k;
   const long avg = (R + E - 1) / E;
   Plan p;
-  // Measured at the config-4 shapes: 8-wave 16- / 32-row tiles for few rows
-  // per expert (T=64: avg 2; T=512: avg 16), 8-wave 128x256 at avg 128
+  // Measured at the config-4 shapes: 16-row tiles for few rows per expert
+  // (T=64: avg 2; the 8-wave 16x256 tile, 1-2% over 16x128), 32-row tiles at
+  // T=512 (avg 16: the 4-wave 32x256 tile, 6-8% over the 8-wave 32x128 one for
+  // FP8 experts; MXFP4 with fp32 activation scales keeps 32x128, 3% faster
+  // there), 8-wave 128x256 at avg 128
   // (T=4096: one m-tile per expert and half the activation re-reads of
   // 128x128; -20% FP8, -4% MXFP4), 8-wave 128x128 between.  At avg 128 the
   // 16x16x128 form of the 128x256 tile (kind 20; 4-register partial sums)
   // folds the block scales 1-2% faster than the 32x32x64 form (kind 17).
-  p.kind = avg <= 8 ? 11 : (avg <= 48 ? 12 : (avg <= 96 ? 15 : 20));
+  p.kind = avg <= 8 ? 10 : (avg <= 48 ? (smode == 2 ? 12 : 4) : (avg <= 96 ? 15 : 20));
   const char* env = getenv("TI_ROCM_MOE_KIND");
   if (env && *env) {
     const int kk = atoi(env);
-    if (kk == 2 || kk == 5 || kk == 6 || kk == 9 || kk == 11 || kk == 12 || kk == 13 || kk == 15 || kk == 16 ||
+    if (kk == 2 || kk == 3 || kk == 4 || kk == 5 || kk == 6 || kk == 9 || kk == 10 || kk == 11 || kk == 12 || kk == 13 ||
+        kk == 15 || kk == 16 ||
         kk == 17 || kk == 20)
       p.kind = kk;
   }
