@@ -826,6 +826,12 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
       // 22.4 -> 15.7 us)
       p.kind = 23;
       splits = 2;
+    } else if (smode == 2 && t < 256 && 2 * tiles(16, 256) <= 256) {
+      // MXFP4 (64-byte e2m1 rows per K step): 8-wave 16x256 tiles split in two
+      // stream more bytes per step for the same workgroup count (config-3-shape
+      // c, N=24576: 22.8 -> 19.8 us)
+      p.kind = 10;
+      splits = 2;
     }
   } else if (smode == 0 && M <= 64 && fill(tiles(64, 224)) > fill(tiles(M <= 32 ? 32 : 64, 128)) + 0.05 &&
              tiles(64, 224) >= 192) {
