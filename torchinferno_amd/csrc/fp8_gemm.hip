@@ -687,20 +687,23 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
 //  23  BM=16  BN=144, 9 waves 1x9 (wave 16x16),   16x16 MFMA            128     6   -- decode, N = 9 * 2^k
 // The 8- and 16-wave kinds put two or four waves on each SIMD, which hides the
 // per-step barrier -> LDS read -> MFMA -> fold latency of one wave.
-// Block mode adds, after the ring, each wave's TM scale products (WGN * BM
-// floats in all).
-template <int BM, int BN, int BK, int WGN, int R, int SMODE>
+// Block mode with deferred folds and the products in LDS (LDS_PROD in the
+// kernel) adds, after the ring, each wave's TM scale products (WGN * BM floats
+// in all).
+template <int BM, int BN, int BK, int WGM, int WGN, int MF, int R, int SMODE>
 constexpr int cfg_lds() {
   const int sa = SMODE >= 1 ? ((BM * 4 + 255) / 256) * 256 : 0;
   constexpr bool f4 = SMODE == 2 || SMODE == 4;
   const int sb = (SMODE == 1 || SMODE == 3) ? 256 : (f4 ? ((BN * 4 + 255) / 256) * 256 : 0);
-  return R * (BM * BK + BN * (f4 ? BK / 2 : BK) + sa + sb) + (SMODE == 1 ? WGN * BM * 4 : 0);
+  constexpr int fm = BM / WGM / MF, fn = BN / WGN / MF, nacc = MF == 32 ? 16 : 4;
+  constexpr bool prod = SMODE == 1 && fm * fn * nacc <= 32 && fm * nacc >= 16;
+  return R * (BM * BK + BN * (f4 ? BK / 2 : BK) + sa + sb) + (prod ? WGN * BM * 4 : 0);
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, int MF, int R, int SMODE, int ODT>
 void launch_cfg(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
-  constexpr int lds = cfg_lds<BM, BN, BK, WGN, R, SMODE>();
-  static_assert(lds <= 160 * 1024, "tile configuration exceeds the 160 KiB LDS");
+  constexpr int lds = cfg_lds<BM, BN, BK, WGM, WGN, MF, R, SMODE>();
+  static_assert(lds <= 160 * 1024 - 256, "tile configuration exceeds the 160 KiB LDS");
   dim3 grid(p.tiles_m * p.tiles_n, p.splits);
   if (p.splits > 1)
     hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, BK, WGM, WGN, MF, R, SMODE, 2, ODT>), grid, dim3(64 * WGM * WGN),
@@ -712,7 +715,8 @@ void launch_cfg(const GemmPlan& p, const GemmArgs& x, hipStream_t stream) {
 
 template <int BM, int BN, int BK, int WGM, int WGN, int MF, int R, int SMODE>
 void launch_grouped_cfg(const GemmArgs& x, int max_mtiles, hipStream_t stream) {
-  constexpr int lds = cfg_lds<BM, BN, BK, WGN, R, SMODE>();
+  constexpr int lds = cfg_lds<BM, BN, BK, WGM, WGN, MF, R, SMODE>();
+  static_assert(lds <= 160 * 1024 - 256, "tile configuration exceeds the 160 KiB LDS");
   dim3 grid((unsigned)(max_mtiles * x.tiles_n), 1);
   hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, BK, WGM, WGN, MF, R, SMODE, 0, TI_DTYPE_BF16>), grid,
                      dim3(64 * WGM * WGN), lds, stream, x);
