@@ -70,3 +70,21 @@ def test_deepseek_module_patch_and_bf16_passthrough():
     assert torch.allclose(mod.linear(x, w), x @ w.t())  # bf16/fp32 weights keep F.linear
     undo()
     assert mod.linear(x, w) == "original"
+
+
+def test_power_of_two_scale_detection(monkeypatch):
+    """Experts take the MFMA-applied scale path (round_scale 2) only when every block
+    scale is a power of two in the E8M0 range and the activation scales are too."""
+    from torchinferno_amd.kernels import moe as tmoe
+    e8 = torch.tensor([1.0, 0.5, 2.0 ** -20]).to(torch.float8_e8m0fnu)
+    assert tmoe._all_pow2(e8)
+    assert tmoe._all_pow2(torch.tensor([[0.25, 4.0], [2.0 ** -127, 1.0]]))
+    assert not tmoe._all_pow2(torch.tensor([0.25, 0.3]))           # not a power of two
+    assert not tmoe._all_pow2(torch.tensor([2.0 ** -128]))         # below E8M0's range
+    assert not tmoe._all_pow2(torch.tensor([0.0]))
+    assert not tmoe._all_pow2(torch.tensor([-0.5]))
+    assert tmoe._round_scale(None, True) == 0
+    assert tmoe._round_scale("ue8m0", False) == 1
+    assert tmoe._round_scale("ue8m0", True) == 2
+    monkeypatch.setenv("TI_ROCM_POW2_MFMA", "0")
+    assert tmoe._round_scale("ue8m0", True) == 1
