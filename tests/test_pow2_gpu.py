@@ -192,3 +192,30 @@ def test_moe_pow2_matches_oracle(dev, monkeypatch, fmt, t, k, kind):
     got = y.float().cpu().numpy()
     assert _rel_err(got, ref) <= 1.5e-2
     assert _rel_err(got, y_fold.float().cpu().numpy()) <= 1.5e-2
+
+
+@pytest.mark.parametrize("entry", ["ti_fp8_gemm_block_pow2", "ti_fp4_gemm_pow2"])
+@pytest.mark.parametrize("m", [5, 300])
+def test_pow2_c_abi_fp16_out(dev, entry, m):
+    """The C ABI's fp16 output on the power-of-two paths: the same fp32 sums as the
+    bf16 output (each output within the rounding of both formats of the other)."""
+    from torchinferno_amd import _lib
+    from torchinferno_amd.kernels import block_fp8 as tb
+    from torchinferno_amd.kernels.fp8 import _ws_args
+    if entry == "ti_fp8_gemm_block_pow2":
+        a, a_s, b, b_s, _, _ = _block_problem(m, 1024, 384, 7, dev)
+        n, k, extra, mode = 384, 1024, (), 3
+    else:
+        _, (a, a_s, b, b_s) = _fp4_inputs(m, 384, 1024, 7, dev)
+        b_s = b_s.view(torch.uint8).contiguous()
+        n, k, extra, mode = 384, 1024, (0,), 4
+    outs = {}
+    for code, dt in ((_lib.TI_DTYPE_BF16, torch.bfloat16), (_lib.TI_DTYPE_F16, torch.float16)):
+        out = torch.empty((m, n), dtype=dt, device=dev)
+        ws, ws_bytes = _ws_args(dev, m, n, k, mode)
+        _lib.call(entry, a.data_ptr(), a_s.data_ptr(), 0, b.data_ptr(), b_s.data_ptr(), *extra, out.data_ptr(),
+                  code, m, n, k, ws, ws_bytes, _lib.stream_of(a))
+        outs[dt] = out.float().cpu().numpy()
+    y16, yb = outs[torch.float16], outs[torch.bfloat16]
+    assert np.isfinite(y16).all()
+    assert np.abs(y16 - yb).max() <= 2 ** -8 * np.abs(yb).max() + 1e-6
