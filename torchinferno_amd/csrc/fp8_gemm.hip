@@ -879,6 +879,10 @@ GemmPlan make_gemm_plan(int M, int N, int K, int smode) {
     // 12-wave 256x96 tiles when they fill the 256 CUs better than 256x128
     // ones (config-2 qkv M=512, N=10240: 214 instead of 160 tiles, 74 -> 60 us)
     p.kind = 22;
+  } else if (smode == 2 && M <= 256 && tiles(256, 128) >= 128) {
+    // MXFP4 at M <= 256: 128x256 tiles (the same workgroup count as 256x128 at
+    // M=256, half the e2m1 slab re-reads): config-3-shape a and c 3-6% faster
+    p.kind = 17;
   } else if (tiles(256, 128) >= (smode >= 1 ? 128 : 144)) {
     p.kind = 9;
   } else if (smode == 0 && tiles(256, 128) >= 64) {
