@@ -1,6 +1,7 @@
 """The C ABI allocates nothing and clears nothing with memsets (split-K tickets
 are left at zero by the kernels themselves), so calls can be captured into a HIP
-graph.  Captured int4 (split-K), FP8 (split-K), fused-producer and MoE calls are
+graph.  Captured int4 (split-K), FP8 (split-K), fused-producer and MoE calls, and
+the power-of-two (E8M0) block GEMM (split-K) and MoE, are
 replayed several times, with eager work and synchronizations between the
 replays, and every replay must equal the eager result bit for bit."""
 import pytest
@@ -15,6 +16,8 @@ def test_graph_replays_match_eager(dev, monkeypatch):
     from torchinferno_amd.kernels import int4 as ti4
     from torchinferno_amd.kernels import moe as tmoe
     from tests.test_moe_gpu import _make_experts
+    from tests.test_pow2_gpu import _fp8_experts_pow2
+    from torchinferno_amd.kernels import block_fp8 as tb
 
     g = torch.Generator(device=dev).manual_seed(3)
     # int4, a split-K plan (narrow N, deep K)
@@ -32,6 +35,13 @@ def test_graph_replays_match_eager(dev, monkeypatch):
     ex = _make_experts(8, 256, 256, 5, dev)
     xm = torch.randn((12, 256), generator=g, device=dev).to(torch.bfloat16)
     logits = torch.randn((12, 8), generator=g, device=dev)
+    # power-of-two scales: a DSv4 block linear (M=3: a split-K plan) and MoE
+    ex2 = _fp8_experts_pow2(8, 256, 256, 6, dev)
+    # finite e4m3 codes only (0x7F and 0xFF are NaN)
+    wb = (torch.randint(0, 0x7E, (512, 1024), generator=g, device=dev)
+          | (torch.randint(0, 2, (512, 1024), generator=g, device=dev) << 7)).to(torch.uint8).view(torch.float8_e4m3fn)
+    wbs = torch.exp2(torch.randint(-12, -8, (4, 8), generator=g, device=dev).float()).to(torch.float8_e8m0fnu)
+    xb = torch.randn((3, 1024), generator=g, device=dev).to(torch.bfloat16)
 
     def run():
         y4 = ti4.int4_mm(a4, q, s, ws4, n4, k4)
@@ -39,7 +49,9 @@ def test_graph_replays_match_eager(dev, monkeypatch):
         y8 = tf8.fp8_per_token_linear_quantized(xq, xs, wq, wsc, out_dtype=torch.bfloat16)
         fq, fs = fused.swiglu_fp8_per_token(*gu.split(2048, dim=-1))
         ym = tmoe.moe_forward(xm, logits, ex, 2)
-        return y4, y8, fq.view(torch.uint8), fs, ym
+        yb = tb.linear(xb, wb, wbs, "ue8m0")
+        ym2 = tmoe.moe_forward(xm, logits, ex2, 2, scale_fmt="ue8m0")
+        return y4, y8, fq.view(torch.uint8), fs, ym, yb, ym2
 
     eager = [t.clone() for t in run()]
     torch.cuda.synchronize()
@@ -55,8 +67,8 @@ def test_graph_replays_match_eager(dev, monkeypatch):
     for rep in range(4):
         graph.replay()
         torch.cuda.synchronize()
-        for got, ref in zip(outs, eager):
-            assert torch.equal(got, ref), f"replay {rep} differs"
+        for i, (got, ref) in enumerate(zip(outs, eager)):
+            assert torch.equal(got, ref), f"replay {rep}: output {i} differs"
         # eager work between replays, using the same workspaces
         assert torch.equal(ti4.int4_mm(a4, q, s, ws4, n4, k4), eager[0])
         torch.cuda.synchronize()
