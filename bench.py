@@ -54,6 +54,55 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def rand_e4m3(shape, device=None, generator=None):
+    """Random finite e4m3fn codes (every byte but the NaN codes 0x7F and 0xFF), as
+    uint8: synthetic FP8 weights and activations."""
+    import torch
+    mag = torch.randint(0, 0x7F, shape, device=device, generator=generator, dtype=torch.uint8)
+    return mag.bitwise_or_(torch.randint(0, 2, shape, device=device, generator=generator, dtype=torch.uint8) << 7)
+
+
+def quant_weight_per_channel(n, k, dev):
+    """Config 2's weight: N(0, 0.02) in bf16, per-output-channel e4m3 (absmax/448),
+    by the package's own quantizer (weight preparation, not timed)."""
+    import torch
+    from torchinferno_amd.kernels import fp8 as tf8
+    wq, ws = tf8.quantize_weight_fp8_per_channel((torch.randn((n, k), device=dev) * 0.02).to(torch.bfloat16))
+    return wq, ws.reshape(-1).float().contiguous()
+
+
+def quant_weight_block(n, k, dev, pow2=False):
+    """Config 3/4's weight: N(0, 0.02) quantized in 128x128 blocks, s = block
+    absmax / 448 (rounded up to a power of two with ``pow2``, DeepSeek-V4's E8M0
+    scales); codes by torch's e4m3 cast.  Returns (codes [n, k], scales fp32
+    [ceil(n/128), k/128])."""
+    import torch
+    nb, kb = -(-n // 128), k // 128
+    w = torch.randn((nb * 128, k), device=dev) * 0.02
+    w[n:] = 0
+    blocks = w.view(nb, 128, kb, 128)
+    amax = blocks.abs().amax(dim=(1, 3))
+    sc = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    if pow2:
+        sc = torch.exp2(torch.ceil(torch.log2(sc)))
+    q = (blocks / sc[:, None, :, None]).view(nb * 128, k)[:n].to(torch.float8_e4m3fn).contiguous()
+    return q, sc.float().contiguous()
+
+
+def quant_act(m, k, dev, mode):
+    """Activations: N(0,1) bf16 rows quantized per token (mode 0) or per 1x128 block
+    with step-major scales [K/128, M] (modes 1-4; power-of-two scales for 3 and 4),
+    by the package's own quantizers."""
+    import torch
+    from torchinferno_amd.kernels import block_fp8 as tb
+    from torchinferno_amd.kernels import fp8 as tf8
+    x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+    if mode == 0:
+        a, asc = tf8.quantize_activation_fp8_per_token(x)
+        return a, asc.reshape(-1).contiguous()
+    return tb._act_quant_stepmajor(x, mode >= 3)
+
+
 def weight_bytes(k, n):
     return k * n // 2 + (k // 128) * n * 2
 
@@ -95,7 +144,7 @@ def cpu_baseline(budget_s: float = 6.0) -> tuple[dict, list]:
     g = torch.Generator().manual_seed(0)
 
     def e4m3(*shape):
-        return torch.randint(-120, 120, shape, generator=g, dtype=torch.int8).view(torch.float8_e4m3fn)
+        return rand_e4m3(shape, generator=g).view(torch.float8_e4m3fn)
 
     # int4 gate_up M=32
     k, n = SHAPES["gate_up"]
@@ -338,20 +387,18 @@ def fp8_points(dev, stream):
                 bs = [fp4_scale_stepmajor(torch.randint(118, 130, (n, k // 32), device=dev, dtype=torch.uint8))
                       for _ in range(ncopy)]
             else:
-                bq = [torch.randint(-120, 120, (n, k), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
-                      for _ in range(ncopy)]
+                # quantized N(0, 0.02) weights, as configs 2 and 3 define them
+                made = [quant_weight_per_channel(n, k, dev) if mode == 0 else quant_weight_block(n, k, dev, pow2)
+                        for _ in range(ncopy)]
+                bq = [q for q, _ in made]
+                bs = [sc for _, sc in made]
+                del made
                 if mode == 0:  # per-token FP8: the weights in the tiled layout the hooks cache
                     bq = [_tiled_fp8_weight(b) for b in bq]
-                bs = [torch.rand((n,) if mode == 0 else (-(-n // 128), k // 128), device=dev) * 1e-3 + 1e-4
-                      for _ in range(ncopy)]
-                if pow2:
-                    bs = [torch.exp2(torch.randint(-13, -9, b.shape, device=dev).float()) for b in bs]
             for m in ms:
-                a = torch.randint(-120, 120, (m, k), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
-                # modes 1-4: step-major activation scales [K/128, M], as the DSv4 linear path keeps them
-                asc = torch.rand((m,) if mode == 0 else (k // 128, m), device=dev) * 0.01 + 1e-3
-                if pow2:
-                    asc = torch.exp2(torch.randint(-10, -6, asc.shape, device=dev).float())
+                # N(0,1) activations quantized per token (config 2) or per 1x128 block with
+                # step-major scales [K/128, M], as the DSv4 linear path keeps them
+                a, asc = quant_act(m, k, dev, mode)
                 out = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
                 i = [0]
 
@@ -433,13 +480,14 @@ def fp8_single_point(spec, launches, dev, stream):
     mode = {"rowcol": 0, "block": 1}[mode_name]
     k, n = (FP8_SHAPES if mode == 0 else BLOCK_SHAPES)[sname]
     ncopy = max(2, -(-ROTATE_BYTES // (n * k)))
-    bq = [torch.randint(-120, 120, (n, k), device=dev, dtype=torch.int8) for _ in range(ncopy)]
+    made = [quant_weight_per_channel(n, k, dev) if mode == 0 else quant_weight_block(n, k, dev)
+            for _ in range(ncopy)]
+    bq = [q for q, _ in made]
+    bs = [sc for _, sc in made]
+    del made
     if mode == 0:
         bq = [_tiled_fp8_weight(b) for b in bq]
-    bs = [torch.rand((n,) if mode == 0 else (-(-n // 128), k // 128), device=dev) * 1e-3 + 1e-4
-          for _ in range(ncopy)]
-    a = torch.randint(-120, 120, (m, k), device=dev, dtype=torch.int8)
-    asc = torch.rand((m,) if mode == 0 else (k // 128, m), device=dev) * 0.01 + 1e-3
+    a, asc = quant_act(m, k, dev, mode)
     out = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
     ws = torch.zeros(64 << 20, dtype=torch.int32, device=dev)
     for i in range(launches):
@@ -463,12 +511,7 @@ def moe_single_point(t, launches, dev, stream, ue8m0=False):
     from torchinferno_amd import _lib
     L = _lib.lib()
     e, h, inter, k = 256, 7168, 2048, 8
-    w13 = torch.randint(-120, 120, (e, 2 * inter, h), device=dev, dtype=torch.int8)
-    w2 = torch.randint(-120, 120, (e, h, inter), device=dev, dtype=torch.int8)
-    s13 = torch.rand((e, 2 * inter // 128, h // 128), device=dev) * 1e-3 + 1e-4
-    s2 = torch.rand((e, h // 128, inter // 128), device=dev) * 1e-3 + 1e-4
-    if ue8m0:
-        s13, s2 = (torch.exp2(torch.randint(-13, -9, s.shape, device=dev).float()) for s in (s13, s2))
+    w13, s13, w2, s2 = fp8_experts(e, h, inter, dev, ue8m0)
     x = torch.randn((t, h), device=dev).to(torch.bfloat16)
     logits = torch.randn((t, e), device=dev)
     wts = torch.empty((t, k), dtype=torch.float32, device=dev)
@@ -534,6 +577,21 @@ def fused_points(dev, stream):
 # --------------------------------------------------------------------------- MoE
 
 
+def fp8_experts(e, h, inter, dev, pow2=False):
+    """Config 4's experts: per expert, w1/w3 [I, H] and w2 [H, I] from N(0, 0.02)
+    quantized in 128x128 blocks (quant_weight_block), stacked as w13 [E, 2I, H],
+    w2 [E, H, I] with their block scales."""
+    import torch
+    w13 = torch.empty((e, 2 * inter, h), device=dev, dtype=torch.float8_e4m3fn)
+    w2 = torch.empty((e, h, inter), device=dev, dtype=torch.float8_e4m3fn)
+    s13 = torch.empty((e, 2 * inter // 128, h // 128), device=dev)
+    s2 = torch.empty((e, h // 128, inter // 128), device=dev)
+    for i in range(e):
+        w13[i], s13[i] = quant_weight_block(2 * inter, h, dev, pow2)
+        w2[i], s2[i] = quant_weight_block(h, inter, dev, pow2)
+    return w13, s13, w2, s2
+
+
 def moe_points(dev, stream):
     """Config 4: router + routed experts (256 experts, H=7168, I=2048, top-8)."""
     import torch
@@ -541,19 +599,19 @@ def moe_points(dev, stream):
     from torchinferno_amd.kernels import moe as tmoe
     L = _lib.lib()
     e, h, inter, k = 256, 7168, 2048, 8
-    w13 = torch.randint(-120, 120, (e, 2 * inter, h), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
-    w2 = torch.randint(-120, 120, (e, h, inter), device=dev, dtype=torch.int8).view(torch.float8_e4m3fn)
-    s13 = torch.rand((e, 2 * inter // 128, h // 128), device=dev) * 1e-3 + 1e-4
-    s2 = torch.rand((e, h // 128, inter // 128), device=dev) * 1e-3 + 1e-4
     recs = []
-    per_expert = 2 * inter * h + h * inter + (s13[0].numel() + s2[0].numel()) * 4
-    recs += _moe_sweep(L, dev, "config4 fp8 moe", "ti_fp8_moe", w13, s13, w2, s2, e, h, inter, k, per_expert)
-    # DeepSeek-V4's scale format: ue8m0 activations and E8M0 weight scales, applied by the MFMA
-    s13, s2 = torch.exp2(torch.randint(-13, -9, s13.shape, device=dev).float()), \
-        torch.exp2(torch.randint(-13, -9, s2.shape, device=dev).float())
-    recs += _moe_sweep(L, dev, "config4-shape fp8 moe ue8m0", "ti_fp8_moe", w13, s13, w2, s2, e, h, inter, k,
-                       per_expert, round_scale=2)
-    del w13, w2, s13, s2
+    for pow2 in (False, True):
+        w13, s13, w2, s2 = fp8_experts(e, h, inter, dev, pow2)
+        per_expert = 2 * inter * h + h * inter + (s13[0].numel() + s2[0].numel()) * 4
+        if not pow2:
+            recs += _moe_sweep(L, dev, "config4 fp8 moe", "ti_fp8_moe", w13, s13, w2, s2, e, h, inter, k,
+                               per_expert)
+        else:
+            # DeepSeek-V4's scale format: ue8m0 activations and E8M0 weight scales, applied by the MFMA
+            recs += _moe_sweep(L, dev, "config4-shape fp8 moe ue8m0", "ti_fp8_moe", w13, s13, w2, s2, e, h,
+                               inter, k, per_expert, round_scale=2)
+        del w13, w2, s13, s2
+        torch.cuda.empty_cache()
     torch.cuda.empty_cache()
     # The same routed experts with MXFP4 weights (e2m1 pairs, e8m0 per 32 K).
     w13 = torch.randint(0, 256, (e, 2 * inter, h // 2), device=dev, dtype=torch.uint8)
@@ -760,7 +818,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (random int4 codes, bf16 scales/activations; random e4m3 codes for FP8; no checkpoint)",
+        "data": ("synthetic (random int4 codes, bf16 scales/activations; FP8 weights and activations quantized "
+                 "from N(0, 0.02) / N(0, 1) as configs 2-4 define them; random e2m1 codes for MXFP4; "
+                 "no checkpoint)"),
         "config": {"workload": "int4 W4A16 g128 decode sweep (BASELINE configs[1])",
                    "shapes": {k: {"K": v[0], "N": v[1]} for k, v in SHAPES.items()},
                    "M": list(MS), "bytes_per_step": step_bytes, "parallelism": "none (1 GPU)"},
