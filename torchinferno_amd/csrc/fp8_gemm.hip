@@ -640,21 +640,35 @@ __global__ __launch_bounds__(64 * WGM * WGN) void fp8_gemm_kernel(GemmArgs x) {
     }
     if (threadIdx.x == 0) __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  // Row / column scales of this lane's outputs, loaded up front with clamped
+  // indices (no load sits behind a bounds branch, so they are all in flight
+  // together), then the stores, unconditional for a per-token tile inside M and
+  // N (measured 2% faster at gate_up M=4096; the scaled modes keep the bounds
+  // test, which measured faster there).
+  float sarow[SMODE == 0 ? FM : 1][MM::NACC], sbcol[SMODE == 0 ? FN : 1];
+  if constexpr (SMODE == 0) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int e = 0; e < MM::NACC; ++e) {
+        const int row = min(m0 + wm * TM + fm * MF + MM::row(e, lane), Mlim - 1);
+        sarow[fm][e] = x.sa[(long)row * x.sa_stride];
+      }
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) sbcol[fn] = x.sb[(long)min(n0 + wn * TN + fn * MF + col_l, N - 1) * x.sb_stride];
+  }
+  const bool inside = SMODE == 0 && m0 + BM <= Mlim && n0 + BN <= N;  // uniform over the workgroup
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) {
       const int col = n0 + wn * TN + fn * MF + col_l;
-      float sbn = 1.f;
-      if constexpr (SMODE == 0) sbn = col < N ? x.sb[(long)col * x.sb_stride] : 0.f;
 #pragma unroll
       for (int e = 0; e < MM::NACC; ++e) {
         const int row = m0 + wm * TM + fm * MF + MM::row(e, lane);
-        if (row < Mlim && col < N) {
-          float v = acc[fm][fn][e];
-          if constexpr (SMODE == 0) v = v * x.sa[(long)row * x.sa_stride] * sbn;
-          x.out[(long)row * N + col] = out_bits<ODT>(v);
-        }
+        float v = acc[fm][fn][e];
+        if constexpr (SMODE == 0) v = v * sarow[fm][e] * sbcol[fn];
+        if (inside || (row < Mlim && col < N)) x.out[(long)row * N + col] = out_bits<ODT>(v);
       }
     }
 }
